@@ -1,0 +1,167 @@
+"""Benchmark of the DSA decode hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2]
+
+A step is one call of ``dsa_amd.kernel`` (the drop-in for the reference's
+``kernel()``, solution/triton/kernel.py:138) on the BASELINE decode workload:
+T=64 tokens, H=16, top-k=2048, ckv512+kpe64 bf16, 131072 slots in pages of 64
+(config 2).  Inputs are synthetic, seeded, and resident in HBM before timing.
+The step is captured once in a HIP graph and replayed, so the figure is the
+GPU time of the path rather than Python/ctypes launch overhead (the eager
+per-call time is reported alongside).  Timing uses HIP events on the stream
+the kernels run on: W untimed warm-up steps, then K timed steps between
+synchronisations.
+
+Prints one JSON line (metric, value in us/call, roofline of the dominant
+kernel, and a CPU baseline: the CPU oracle timed on this host).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "flashinfer-repo_amd")]
+
+METRIC = "µs/call + HBM GB/s & MFMA %, DSA decode H=16 topk=2048 T=64"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="cfg2", choices=["cfg1", "cfg2", "cfg3", "cfg4"])
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="budget of the CPU-oracle baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def cpu_baseline(d, budget_s: float):
+    """Times the CPU oracle (the restatement of the reference's run()) on the
+    same workload, whole calls, until the budget is spent."""
+    import numpy as np
+    import torch
+
+    import oracle
+
+    def bits(t):
+        return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+    args = (bits(d["q_nope"]), bits(d["q_pe"]), bits(d["ckv_cache"]), bits(d["kpe_cache"]),
+            d["sparse_indices"].numpy(), d["sm_scale"])
+    threads = min(16, os.cpu_count() or 1)
+    oracle.attention(*args, nthreads=threads)  # warm-up (page-in, thread pool)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        oracle.attention(*args, nthreads=threads)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 1000:
+            break
+    T = d["q_nope"].shape[0]
+    return {"value": el / n * 1e6, "unit": "µs/call", "cores": threads, "kind": "port",
+            "sample": f"{n} full calls of the {T}-token workload (fp64 CPU oracle, OpenMP "
+                      f"{threads} threads, {el:.1f} s)"}
+
+
+def main():
+    a = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if a.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (asked for {max(a.gpus, world)}); "
+              "the DSA path shards by tokens/heads with no exchange and is benchmarked at N=1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from dsa_amd import kernel, num_splits, workloads
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    d = workloads.CONFIGS[a.config]()
+    g = workloads.to_device(d, dev)
+    T, H, _ = d["q_nope"].shape
+    K = d["sparse_indices"].shape[1]
+    args = (g["q_nope"], g["q_pe"], g["ckv_cache"], g["kpe_cache"], g["sparse_indices"],
+            d["sm_scale"])
+    alg_bytes = workloads.attention_bytes(d["sparse_indices"])
+    alg_flops = workloads.attention_flops(d["sparse_indices"], H)
+
+    # eager warm-up, then capture one step
+    for _ in range(3):
+        kernel(*args)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        kernel(*args)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        kernel(*args)
+    torch.cuda.synchronize()
+
+    for _ in range(a.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(a.steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms_per_step = start.elapsed_time(end) / a.steps
+
+    # eager (Python shim + ctypes + launches) for reference
+    start.record()
+    for _ in range(a.steps):
+        kernel(*args)
+    end.record()
+    torch.cuda.synchronize()
+    eager_ms = start.elapsed_time(end) / a.steps
+
+    us = ms_per_step * 1e3
+    gbs = alg_bytes / (ms_per_step * 1e-3) / 1e9
+    tflops = alg_flops / (ms_per_step * 1e-3) / 1e12
+    splits = num_splits(T, H, K)
+    line = {
+        "metric": METRIC,
+        "value": round(us, 3),
+        "unit": "µs/call",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded; q~N(0,1), cache~N(0,0.5), distinct slots per token)",
+        "config": {"workload": f"{a.config}: DSA sparse attention T={T} H={H} topk={K} "
+                               f"ckv512+kpe64 bf16, {d['ckv_cache'].numel() // 512} slots, "
+                               f"page_size={d['ckv_cache'].shape[1]}",
+                   "tokens": T, "heads": H, "topk": K, "splits": splits,
+                   "timing": "HIP-graph replay of one kernel() call per step",
+                   "eager_us_per_call": round(eager_ms * 1e3, 3)},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": alg_bytes,
+                     "kernel": "dsa_attn_partial_kernel+dsa_attn_combine_kernel (whole step)"},
+        "mfma": {"achieved_tflops": round(tflops, 2), "peak_tflops": BF16_PEAK_TFLOPS,
+                 "frac": round(tflops / BF16_PEAK_TFLOPS, 5), "algorithmic_flops": alg_flops},
+    }
+    if not a.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(d, a.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

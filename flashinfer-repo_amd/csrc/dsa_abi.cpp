@@ -1,0 +1,180 @@
+// dsa_abi.cpp -- the extern "C" boundary of libdsa_amd.so (declared in
+// include/dsa_abi.h).  Validates shapes, strides and alignment on the host,
+// chooses the launch configuration from shapes alone (no device reads, no
+// synchronisation, no allocation) and enqueues the HIP kernels on the
+// caller's stream.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/dsa_abi.h"
+#include "dsa_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return DSA_OK;
+}
+
+bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Top-k chunk length per split and the split count that results.  Automatic
+// mode aims for about one workgroup per compute unit while keeping at least
+// one 32-key tile per wave; an explicit request is honoured up to one key per
+// split (the reference's kernel_splitk additionally required topk % SPLIT_K
+// == 0, kernel.py:512; uneven chunks are fine here).
+void choose_splits(int64_t T, int64_t H, int64_t K, int32_t requested, int32_t *splits,
+                   int32_t *chunk) {
+  if (K <= 0) {
+    *splits = 1;
+    *chunk = 0;
+    return;
+  }
+  int64_t S;
+  int64_t c;
+  if (requested > 0) {
+    S = requested < K ? requested : K;
+    c = ceil_div(K, S);
+  } else {
+    const int64_t units = (T > 0 ? T : 1) * (H / dsa::kHeadsPerGroup > 0 ? H / dsa::kHeadsPerGroup : 1);
+    const int64_t tiles = ceil_div(K, dsa::kKeysPerTile);
+    const int64_t max_s = ceil_div(tiles, dsa::kAttnWaves);
+    S = ceil_div(dsa::kNumCU, units);
+    if (S > max_s) S = max_s;
+    if (S < 1) S = 1;
+    c = ceil_div(tiles, S) * dsa::kKeysPerTile;
+  }
+  S = ceil_div(K, c);
+  *splits = (int32_t)S;
+  *chunk = (int32_t)c;
+}
+
+size_t attn_workspace(int64_t T, int64_t H, int32_t S) {
+  if (S <= 1) return 0;
+  const size_t rows = (size_t)T * (size_t)S * (size_t)H;
+  return rows * dsa::kHeadDimCkv * sizeof(float) + rows * 2 * sizeof(float);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *dsa_last_error(void) { return g_last_error.c_str(); }
+
+int dsa_abi_version(void) { return DSA_ABI_VERSION; }
+
+int32_t dsa_attn_num_splits(int64_t num_tokens, int64_t num_heads, int64_t topk,
+                            int32_t requested) {
+  int32_t s, c;
+  choose_splits(num_tokens, num_heads, topk, requested, &s, &c);
+  return s;
+}
+
+size_t dsa_attn_workspace_bytes(int64_t num_tokens, int64_t num_heads, int64_t topk,
+                                int32_t requested_splits) {
+  int32_t s, c;
+  choose_splits(num_tokens, num_heads, topk, requested_splits, &s, &c);
+  return attn_workspace(num_tokens, num_heads, s);
+}
+
+int dsa_attn_fwd(const dsa_attn_args *a, void *stream) {
+  if (!a) return fail(DSA_EINVAL, "dsa_attn_fwd: args is NULL");
+  if (a->head_dim_ckv != dsa::kHeadDimCkv || a->head_dim_kpe != dsa::kHeadDimKpe)
+    return fail(DSA_EUNSUPPORTED, "dsa_attn_fwd: head dims must be ckv=512, kpe=64 (got %lld, %lld)",
+                (long long)a->head_dim_ckv, (long long)a->head_dim_kpe);
+  if (a->num_tokens < 0 || a->num_heads <= 0 || a->topk < 0 || a->page_size <= 0 ||
+      a->num_pages < 0)
+    return fail(DSA_EINVAL, "dsa_attn_fwd: negative or zero size (T=%lld H=%lld topk=%lld "
+                "page_size=%lld num_pages=%lld)", (long long)a->num_tokens,
+                (long long)a->num_heads, (long long)a->topk, (long long)a->page_size,
+                (long long)a->num_pages);
+  if (a->num_heads % dsa::kHeadsPerGroup != 0)
+    return fail(DSA_EUNSUPPORTED, "dsa_attn_fwd: num_heads must be a multiple of 16 (got %lld)",
+                (long long)a->num_heads);
+  if (a->num_tokens > (1 << 26) || a->topk > (1 << 30) || a->num_heads > 4096 ||
+      a->page_size > (1 << 30))
+    return fail(DSA_EUNSUPPORTED, "dsa_attn_fwd: size beyond the supported range");
+  if (a->num_splits < 0) return fail(DSA_EINVAL, "dsa_attn_fwd: num_splits must be >= 0");
+  if (a->num_tokens == 0) return ok();
+  if (!a->q_nope || !a->q_pe || !a->sparse_indices || !a->output || !a->lse)
+    return fail(DSA_EINVAL, "dsa_attn_fwd: NULL tensor pointer");
+  if (a->num_pages > 0 && (!a->ckv || !a->kpe))
+    return fail(DSA_EINVAL, "dsa_attn_fwd: NULL cache pointer");
+  // 16-byte rows for the MFMA operand loads and the LDS DMA gathers.
+  if (!aligned(a->q_nope, 16) || !aligned(a->q_pe, 16) || !aligned(a->ckv, 16) ||
+      !aligned(a->kpe, 16) || (a->q_nope_stride_t * 2) % 16 || (a->q_nope_stride_h * 2) % 16 ||
+      (a->q_pe_stride_t * 2) % 16 || (a->q_pe_stride_h * 2) % 16 ||
+      (a->ckv_stride_page * 2) % 16 || (a->ckv_stride_tok * 2) % 16 ||
+      (a->kpe_stride_page * 2) % 16 || (a->kpe_stride_tok * 2) % 16)
+    return fail(DSA_EINVAL, "dsa_attn_fwd: q/ckv/kpe rows must be 16-byte aligned");
+  if (!aligned(a->output, 8) || (a->out_stride_t * 2) % 8 || (a->out_stride_h * 2) % 8 ||
+      !aligned(a->lse, 4) || !aligned(a->sparse_indices, 4))
+    return fail(DSA_EINVAL, "dsa_attn_fwd: output rows must be 8-byte aligned");
+  const int64_t num_slots = a->num_pages * a->page_size;
+
+  int32_t S, chunk;
+  choose_splits(a->num_tokens, a->num_heads, a->topk, a->num_splits, &S, &chunk);
+  if (a->num_tokens * (int64_t)S > 0x7fffffffLL)
+    return fail(DSA_EUNSUPPORTED, "dsa_attn_fwd: num_tokens * splits exceeds the grid");
+  const size_t need = attn_workspace(a->num_tokens, a->num_heads, S);
+  if (need > 0 && (!a->workspace || a->workspace_bytes < need || !aligned(a->workspace, 16)))
+    return fail(DSA_EWORKSPACE, "dsa_attn_fwd: workspace of %zu bytes (16-byte aligned) needed, "
+                "got %zu", need, a->workspace ? a->workspace_bytes : (size_t)0);
+
+  dsa::AttnParams p;
+  p.q_nope = static_cast<const char *>(a->q_nope);
+  p.qn_st = a->q_nope_stride_t * 2;
+  p.qn_sh = a->q_nope_stride_h * 2;
+  p.q_pe = static_cast<const char *>(a->q_pe);
+  p.qp_st = a->q_pe_stride_t * 2;
+  p.qp_sh = a->q_pe_stride_h * 2;
+  p.ckv = static_cast<const char *>(a->ckv);
+  p.ckv_sp = a->ckv_stride_page * 2;
+  p.ckv_so = a->ckv_stride_tok * 2;
+  p.kpe = static_cast<const char *>(a->kpe);
+  p.kpe_sp = a->kpe_stride_page * 2;
+  p.kpe_so = a->kpe_stride_tok * 2;
+  p.idx = a->sparse_indices;
+  p.idx_st = a->idx_stride_t;
+  p.out = static_cast<char *>(a->output);
+  p.out_st = a->out_stride_t * 2;
+  p.out_sh = a->out_stride_h * 2;
+  p.lse = a->lse;
+  p.lse_st = a->lse_stride_t;
+  p.lse_sh = a->lse_stride_h;
+  p.T = (int32_t)a->num_tokens;
+  p.H = (int32_t)a->num_heads;
+  p.K = (int32_t)a->topk;
+  p.page_size = (int32_t)a->page_size;
+  p.num_slots = num_slots;
+  p.scale_log2 = a->sm_scale * 1.4426950408889634f;
+  p.num_splits = S;
+  p.chunk = chunk;
+  float *ws = static_cast<float *>(a->workspace);
+  p.part_acc = ws;
+  p.part_ml = ws ? ws + (size_t)a->num_tokens * S * a->num_heads * dsa::kHeadDimCkv : nullptr;
+
+  const hipError_t e = dsa::launch_attention(p, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess)
+    return fail(DSA_ELAUNCH, "dsa_attn_fwd: launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+}  // extern "C"

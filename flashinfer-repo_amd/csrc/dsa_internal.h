@@ -1,0 +1,64 @@
+// dsa_internal.h -- shared declarations between the C-ABI layer and the HIP
+// kernels of libdsa_amd.so (not part of the public ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dsa {
+
+// MI355X (gfx950): 256 compute units in 8 XCDs.  The automatic split count is
+// derived from this constant so that the workspace size a caller queries on
+// the host without a device agrees with what the launch uses.
+constexpr int kNumCU = 256;
+
+constexpr int kHeadDimCkv = 512;
+constexpr int kHeadDimKpe = 64;
+constexpr int kHeadsPerGroup = 16;  // MFMA N dimension: one 16-head group
+constexpr int kKeysPerTile = 32;    // keys one wave gathers and consumes per step
+constexpr int kAttnWaves = 4;       // waves per workgroup (independent key streams)
+
+struct AttnParams {
+  const char *q_nope;  // byte strides below
+  int64_t qn_st, qn_sh;
+  const char *q_pe;
+  int64_t qp_st, qp_sh;
+  const char *ckv;
+  int64_t ckv_sp, ckv_so;
+  const char *kpe;
+  int64_t kpe_sp, kpe_so;
+  const int32_t *idx;  // element stride
+  int64_t idx_st;
+  char *out;
+  int64_t out_st, out_sh;
+  float *lse;  // element strides
+  int64_t lse_st, lse_sh;
+  int32_t T, H, K, page_size;
+  int64_t num_slots;
+  float scale_log2;  // sm_scale * log2(e)
+  int32_t num_splits, chunk;
+  float *part_acc;  // [T][S][H][512] unnormalised partial outputs
+  float *part_ml;   // [T][S][H][2]   (running max in log2 units, sum)
+};
+
+hipError_t launch_attention(const AttnParams &p, hipStream_t stream);
+
+struct IndexerParams {
+  const uint8_t *q;       // [T][Hi][128] e4m3 codes
+  const uint8_t *k;       // [S][128] e4m3 codes
+  const float *k_scale;   // [S]
+  const float *w;         // [T][Hi]
+  const int32_t *limit;   // [T]
+  int32_t T, Hi, S, topk;
+  const int32_t *block_table;
+  int64_t bt_stride;
+  int32_t page_size;
+  int32_t *out;           // [T][topk]
+  float *scores;          // [T][S] (workspace or caller buffer)
+  int8_t *q_pieces;       // workspace: [T][Hi/16][3][16 heads][128] int8
+  int32_t *q_flags;       // workspace: [T] highest nonzero piece of q
+};
+
+hipError_t launch_indexer(const IndexerParams &p, hipStream_t stream);
+
+}  // namespace dsa

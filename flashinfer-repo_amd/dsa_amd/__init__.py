@@ -1,0 +1,14 @@
+"""dsa_amd -- MI355X (gfx950) DeepSeek sparse attention hot path.
+
+Hand-written HIP kernels behind a C ABI (``include/dsa_abi.h``,
+``libdsa_amd.so``) with a host-side mirror of the reference's entry points:
+
+* ``dsa_amd.kernel``: ``kernel``, ``kernel_splitk``, ``kernel_splitk_v2``,
+  ``kernel_out`` (reference ``solution/triton/kernel.py``)
+* ``dsa_amd.indexer_kernel``: ``run_indexer_and_topk`` and the pipeline
+  (reference ``solution/triton/indexer_kernel.py``)
+* ``dsa_amd.workloads``: seeded synthetic inputs for the benchmark configs
+"""
+from .kernel import kernel, kernel_out, kernel_splitk, kernel_splitk_v2, num_splits  # noqa: F401
+
+__all__ = ["kernel", "kernel_splitk", "kernel_splitk_v2", "kernel_out", "num_splits"]

@@ -1,0 +1,155 @@
+"""Host-side mirror of the reference's DSA attention entry points.
+
+Same names, arguments and return values as ``solution/triton/kernel.py`` of the
+reference, so its drivers (``test_splitk_correctness.py``,
+``profile_kernel*.py``) run unchanged against this module:
+
+* :func:`kernel`            -- ``kernel.py:138-182``
+* :func:`kernel_splitk`     -- ``kernel.py:496-567``
+* :func:`kernel_splitk_v2`  -- ``kernel.py:707-799``
+* :func:`kernel_out`        -- destination-passing variant (``output``/``lse``
+  appended, the flashinfer-bench DPS convention)
+
+All of them call the HIP library through its C ABI (``dsa_attn_fwd``); the
+tensors only supply device pointers, strides and the current stream.  The
+reference's constant asserts (H=16, page_size=64, topk=2048,
+``kernel.py:147-151``) are relaxed to what the kernels implement: any number of
+tokens and pages, any page size and top-k, H a multiple of 16, head dims
+512/64.  Shape or dtype errors raise ``ValueError`` before anything is
+enqueued.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+HEAD_DIM_CKV = 512
+HEAD_DIM_KPE = 64
+
+
+def _stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _inner_contiguous(x: torch.Tensor) -> torch.Tensor:
+    return x if x.stride(-1) == 1 else x.contiguous()
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _cache_view(cache: torch.Tensor, dim: int, name: str) -> Tuple[torch.Tensor, int, int, int, int]:
+    """Return (tensor, num_pages, page_size, stride_page, stride_tok) for a
+    paged cache ``[pages, page_size, dim]`` or a flat ``[slots, dim]`` one."""
+    _check(cache.dtype == torch.bfloat16, f"{name} must be bfloat16, got {cache.dtype}")
+    _check(cache.shape[-1] == dim, f"{name} last dim must be {dim}, got {tuple(cache.shape)}")
+    cache = _inner_contiguous(cache)
+    if cache.dim() == 3:
+        return cache, cache.shape[0], cache.shape[1], cache.stride(0), cache.stride(1)
+    if cache.dim() == 2:
+        return cache, cache.shape[0], 1, cache.stride(0), cache.stride(0)
+    raise ValueError(f"{name} must be [pages, page_size, {dim}] or [slots, {dim}]")
+
+
+def _attention(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, num_splits: int,
+               output: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None):
+    _check(q_nope.dim() == 3 and q_pe.dim() == 3, "q_nope/q_pe must be [T, H, D]")
+    T, H, dc = q_nope.shape
+    _check(dc == HEAD_DIM_CKV, f"q_nope head dim must be {HEAD_DIM_CKV}, got {dc}")
+    _check(tuple(q_pe.shape) == (T, H, HEAD_DIM_KPE),
+           f"q_pe must be [{T}, {H}, {HEAD_DIM_KPE}], got {tuple(q_pe.shape)}")
+    _check(q_nope.dtype == torch.bfloat16 and q_pe.dtype == torch.bfloat16,
+           "q_nope/q_pe must be bfloat16")
+    _check(H % 16 == 0, f"num heads must be a multiple of 16, got {H}")
+    _check(sparse_indices.dim() == 2 and sparse_indices.shape[0] == T,
+           f"sparse_indices must be [{T}, topk], got {tuple(sparse_indices.shape)}")
+    _check(sparse_indices.dtype == torch.int32, "sparse_indices must be int32")
+    dev = q_nope.device
+    _check(dev.type == "cuda", "tensors must live on a GPU device")
+    for name, x in (("q_pe", q_pe), ("ckv_cache", ckv_cache), ("kpe_cache", kpe_cache),
+                    ("sparse_indices", sparse_indices)):
+        _check(x.device == dev, f"{name} is on {x.device}, expected {dev}")
+    ckv, pages, ps, ckv_sp, ckv_so = _cache_view(ckv_cache, HEAD_DIM_CKV, "ckv_cache")
+    kpe, kpages, kps, kpe_sp, kpe_so = _cache_view(kpe_cache, HEAD_DIM_KPE, "kpe_cache")
+    _check((pages, ps) == (kpages, kps), "ckv_cache and kpe_cache page layouts differ")
+    if isinstance(sm_scale, torch.Tensor):
+        sm_scale = float(sm_scale.item())
+    q_nope = _inner_contiguous(q_nope)
+    q_pe = _inner_contiguous(q_pe)
+    idx = _inner_contiguous(sparse_indices)
+    K = idx.shape[1]
+
+    if output is None:
+        output = torch.empty((T, H, HEAD_DIM_CKV), dtype=torch.bfloat16, device=dev)
+    if lse is None:
+        lse = torch.empty((T, H), dtype=torch.float32, device=dev)
+    _check(tuple(output.shape) == (T, H, HEAD_DIM_CKV) and output.dtype == torch.bfloat16
+           and output.stride(-1) == 1 and output.device == dev,
+           "output must be a [T, H, 512] bfloat16 tensor with a contiguous last dim")
+    _check(tuple(lse.shape) == (T, H) and lse.dtype == torch.float32 and lse.device == dev,
+           "lse must be a [T, H] float32 tensor")
+
+    lib = _lib.load()
+    ws_bytes = lib.dsa_attn_workspace_bytes(T, H, K, int(num_splits))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes else None
+
+    a = _lib.AttnArgs()
+    a.q_nope, a.q_nope_stride_t, a.q_nope_stride_h = q_nope.data_ptr(), q_nope.stride(0), q_nope.stride(1)
+    a.q_pe, a.q_pe_stride_t, a.q_pe_stride_h = q_pe.data_ptr(), q_pe.stride(0), q_pe.stride(1)
+    a.ckv, a.ckv_stride_page, a.ckv_stride_tok = ckv.data_ptr(), ckv_sp, ckv_so
+    a.kpe, a.kpe_stride_page, a.kpe_stride_tok = kpe.data_ptr(), kpe_sp, kpe_so
+    a.sparse_indices, a.idx_stride_t = idx.data_ptr(), idx.stride(0)
+    a.output, a.out_stride_t, a.out_stride_h = output.data_ptr(), output.stride(0), output.stride(1)
+    a.lse, a.lse_stride_t, a.lse_stride_h = lse.data_ptr(), lse.stride(0), lse.stride(1)
+    a.num_tokens, a.num_heads, a.topk = T, H, K
+    a.page_size, a.num_pages = ps, pages
+    a.head_dim_ckv, a.head_dim_kpe = HEAD_DIM_CKV, HEAD_DIM_KPE
+    a.sm_scale = float(sm_scale)
+    a.num_splits = int(num_splits)
+    a.workspace = ws.data_ptr() if ws is not None else None
+    a.workspace_bytes = ws_bytes
+    _lib.check("dsa_attn_fwd", lib.dsa_attn_fwd(ctypes.byref(a), _stream_handle(dev)))
+    return output, lse
+
+
+def kernel(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale):
+    """Sparse MLA attention (reference ``kernel.py:138``).
+
+    Returns ``(output [T,H,512] bf16, lse [T,H] fp32 base-2)``.  The split of
+    the top-k axis over workgroups is chosen automatically to fill the GPU.
+    """
+    return _attention(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, 0)
+
+
+def kernel_splitk(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, SPLIT_K=16):
+    """Split-K variant (reference ``kernel.py:496``): the top-k axis is cut into
+    ``SPLIT_K`` chunks computed in parallel and merged with log-sum-exp
+    weights.  Unlike the reference, ``topk % SPLIT_K`` need not be 0."""
+    _check(int(SPLIT_K) >= 1, f"SPLIT_K must be >= 1, got {SPLIT_K}")
+    return _attention(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, int(SPLIT_K))
+
+
+def kernel_splitk_v2(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, SPLIT_K=16):
+    """Reference ``kernel.py:707``: same result as :func:`kernel_splitk`.  The
+    reference's three-phase merge with fp32 atomics (``kernel.py:583-704``) is
+    replaced by the one deterministic merge kernel."""
+    return kernel_splitk(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, SPLIT_K)
+
+
+def kernel_out(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, output, lse,
+               num_splits: int = 0):
+    """Destination-passing variant: writes into ``output`` and ``lse``."""
+    _attention(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, int(num_splits),
+               output=output, lse=lse)
+    return output, lse
+
+
+def num_splits(num_tokens: int, num_heads: int, topk: int, requested: int = 0) -> int:
+    """Split count :func:`kernel` (requested=0) or :func:`kernel_splitk` uses."""
+    return int(_lib.load().dsa_attn_num_splits(num_tokens, num_heads, topk, requested))

@@ -1,0 +1,182 @@
+"""Seeded synthetic workloads for the five BASELINE configurations.
+
+Inputs are generated on the CPU with ``torch.Generator().manual_seed(seed)``
+(sampled in fp32, then cast), so a CPU checker and the GPU see identical bits
+after ``.to(device)``.  ``N(0, v)`` below means variance ``v``.
+
+cfg1  T=4, H=16, 4096 slots, page_size=1, topk=256; row 3's last 56 ids = -1.
+cfg2  decode: T=64, H=16, topk=2048, 131072 slots in pages of 64, one shared
+      random page permutation as block table; token t's context length
+      L_t ~ U[1024, 131072]; min(L_t, 2048) distinct positions < L_t mapped
+      through the block table, -1 padded.
+cfg3  prefill: T=2048, same cache; query i selects 2048 distinct positions
+      <= 32768 + i.
+cfg4  T=256, H=128, 65536 slots, page_size=64; 5% of cache rows scaled x8;
+      10% of rows get a random tail of -1.
+cfg5  indexer: q_idx [64,64,128] and k_idx [32768,128] e4m3fn (N(0,1) cast),
+      k_scale ~ U(0.5, 2), weights ~ N(0, 1/8); causal limit 32768-64+t;
+      top-2048 positions feed the cfg2 attention through its block table.
+"""
+from __future__ import annotations
+
+import math
+from typing import Dict
+
+import torch
+
+SM_SCALE = 1.0 / math.sqrt(192.0)
+DEFAULT_SEED = 1000
+
+
+def _gen(seed: int) -> torch.Generator:
+    g = torch.Generator()
+    g.manual_seed(int(seed))
+    return g
+
+
+def _normal(shape, var: float, g: torch.Generator) -> torch.Tensor:
+    return torch.randn(shape, generator=g, dtype=torch.float32) * math.sqrt(var)
+
+
+def _distinct_below(n: int, k: int, g: torch.Generator) -> torch.Tensor:
+    """k distinct integers drawn uniformly from [0, n) (k <= n)."""
+    if n <= 4 * k:
+        return torch.randperm(n, generator=g)[:k]
+    # rejection-free for sparse draws: oversample, dedupe, keep first k in draw order
+    while True:
+        cand = torch.randint(0, n, (2 * k,), generator=g)
+        uniq, inv = torch.unique(cand, return_inverse=True)
+        first = torch.full((uniq.numel(),), 2 * k, dtype=torch.long)
+        first.scatter_reduce_(0, inv, torch.arange(2 * k), reduce="amin")
+        order = torch.argsort(first)
+        if order.numel() >= k:
+            return uniq[order[:k]]
+
+
+def attention_inputs(T: int, H: int, topk: int, num_pages: int, page_size: int, seed: int,
+                     cache_var: float = 0.5) -> Dict[str, torch.Tensor]:
+    g = _gen(seed)
+    q_nope = _normal((T, H, 512), 1.0, g).to(torch.bfloat16)
+    q_pe = _normal((T, H, 64), 1.0, g).to(torch.bfloat16)
+    ckv = _normal((num_pages, page_size, 512), cache_var, g).to(torch.bfloat16)
+    kpe = _normal((num_pages, page_size, 64), cache_var, g).to(torch.bfloat16)
+    return {"q_nope": q_nope, "q_pe": q_pe, "ckv_cache": ckv, "kpe_cache": kpe, "gen": g}
+
+
+def cfg1(seed: int = DEFAULT_SEED + 1) -> Dict[str, object]:
+    d = attention_inputs(4, 16, 256, 4096, 1, seed)
+    g = d.pop("gen")
+    idx = torch.stack([torch.randperm(4096, generator=g)[:256] for _ in range(4)]).to(torch.int32)
+    idx[3, 200:] = -1
+    d.update(sparse_indices=idx, sm_scale=SM_SCALE, name="cfg1")
+    return d
+
+
+def _block_table(num_pages: int, g: torch.Generator) -> torch.Tensor:
+    return torch.randperm(num_pages, generator=g).to(torch.int32)
+
+
+def positions_to_slots(pos: torch.Tensor, block_table: torch.Tensor, page_size: int) -> torch.Tensor:
+    """Logical positions -> physical slot ids through a block table (-1 kept)."""
+    p = pos.to(torch.int64)
+    valid = p >= 0
+    pc = torch.where(valid, p, torch.zeros_like(p))
+    slot = block_table.to(torch.int64)[pc // page_size] * page_size + pc % page_size
+    return torch.where(valid, slot, torch.full_like(slot, -1)).to(torch.int32)
+
+
+def cfg2(seed: int = DEFAULT_SEED + 2, T: int = 64) -> Dict[str, object]:
+    num_pages, ps, K = 2048, 64, 2048
+    d = attention_inputs(T, 16, K, num_pages, ps, seed)
+    g = d.pop("gen")
+    bt = _block_table(num_pages, g)
+    lens = torch.randint(1024, num_pages * ps + 1, (T,), generator=g)
+    pos = torch.full((T, K), -1, dtype=torch.int64)
+    for t in range(T):
+        n = min(int(lens[t]), K)
+        pos[t, :n] = _distinct_below(int(lens[t]), n, g)
+    d.update(sparse_indices=positions_to_slots(pos, bt, ps), block_table=bt, context_lens=lens,
+             sm_scale=SM_SCALE, name="cfg2")
+    return d
+
+
+def cfg3(seed: int = DEFAULT_SEED + 3, T: int = 2048, ctx_start: int = 32768) -> Dict[str, object]:
+    num_pages, ps, K = 2048, 64, 2048
+    d = attention_inputs(T, 16, K, num_pages, ps, seed)
+    g = d.pop("gen")
+    bt = _block_table(num_pages, g)
+    pos = torch.empty((T, K), dtype=torch.int64)
+    for i in range(T):
+        pos[i] = _distinct_below(ctx_start + i + 1, K, g)
+    d.update(sparse_indices=positions_to_slots(pos, bt, ps), block_table=bt,
+             sm_scale=SM_SCALE, name="cfg3")
+    return d
+
+
+def cfg4(seed: int = DEFAULT_SEED + 4, T: int = 256) -> Dict[str, object]:
+    num_pages, ps, K, H = 1024, 64, 2048, 128
+    d = attention_inputs(T, H, K, num_pages, ps, seed, cache_var=0.5)
+    g = d.pop("gen")
+    slots = num_pages * ps
+    outl = torch.randperm(slots, generator=g)[: slots // 20]
+    ckv = d["ckv_cache"].view(slots, 512).float()
+    kpe = d["kpe_cache"].view(slots, 64).float()
+    ckv[outl] *= 8.0
+    kpe[outl] *= 8.0
+    d["ckv_cache"] = ckv.to(torch.bfloat16).view(num_pages, ps, 512)
+    d["kpe_cache"] = kpe.to(torch.bfloat16).view(num_pages, ps, 64)
+    idx = torch.stack([_distinct_below(slots, K, g) for _ in range(T)]).to(torch.int32)
+    padded = torch.randperm(T, generator=g)[: T // 10]
+    for t in padded.tolist():
+        n_pad = int(torch.randint(1, K, (1,), generator=g))
+        idx[t, K - n_pad:] = -1
+    d.update(sparse_indices=idx, sm_scale=SM_SCALE, name="cfg4")
+    return d
+
+
+def e4m3(x: torch.Tensor) -> torch.Tensor:
+    """fp32 -> e4m3fn codes (uint8), torch's round-to-nearest-even cast."""
+    return x.to(torch.float8_e4m3fn).view(torch.uint8)
+
+
+def indexer_inputs(T: int = 64, Hi: int = 64, D: int = 128, S: int = 32768, seed: int = 0,
+                   ctx_end: int = None) -> Dict[str, torch.Tensor]:
+    g = _gen(seed)
+    q = e4m3(_normal((T, Hi, D), 1.0, g))
+    k = e4m3(_normal((S, D), 1.0, g))
+    scale = torch.rand((S,), generator=g, dtype=torch.float32) * 1.5 + 0.5
+    w = _normal((T, Hi), 1.0 / 8.0, g)
+    end = S if ctx_end is None else ctx_end
+    limit = (end - T + torch.arange(T)).to(torch.int32)
+    return {"q_idx": q, "k_idx": k, "k_scale": scale, "weights": w, "causal_limit": limit}
+
+
+def cfg5(seed: int = DEFAULT_SEED + 5) -> Dict[str, object]:
+    d = indexer_inputs(seed=seed)
+    att = cfg2(seed=seed + 100)
+    att.pop("sparse_indices")
+    d.update({("attn_" + k if k == "name" else k): v for k, v in att.items()})
+    d.update(topk=2048, page_size=64, name="cfg5")
+    return d
+
+
+CONFIGS = {"cfg1": cfg1, "cfg2": cfg2, "cfg3": cfg3, "cfg4": cfg4, "cfg5": cfg5}
+
+
+def to_device(d: Dict[str, object], device) -> Dict[str, object]:
+    return {k: (v.to(device) if isinstance(v, torch.Tensor) else v) for k, v in d.items()}
+
+
+def gathered_rows(sparse_indices: torch.Tensor) -> int:
+    """Number of valid (non -1) entries: the rows the attention gathers."""
+    return int((sparse_indices >= 0).sum())
+
+
+def attention_bytes(sparse_indices: torch.Tensor) -> int:
+    """Algorithmic gathered KV bytes: 1152 B (512+64 bf16) per valid entry."""
+    return gathered_rows(sparse_indices) * (512 + 64) * 2
+
+
+def attention_flops(sparse_indices: torch.Tensor, H: int) -> int:
+    """Algorithmic FLOPs: 2*H*(576+512) per valid entry."""
+    return gathered_rows(sparse_indices) * 2 * H * (576 + 512)

@@ -1,0 +1,148 @@
+/*
+ * dsa_abi.h -- C ABI of the MI355X (gfx950) DeepSeek sparse attention (DSA)
+ * library libdsa_amd.so.
+ *
+ * Every entry point takes plain device pointers, element strides and sizes;
+ * no framework types cross this boundary.  Calls enqueue work on `stream`
+ * (a hipStream_t; NULL = the default stream), never synchronize, never
+ * allocate and never free.  Status 0 = success; otherwise dsa_last_error()
+ * (thread-local) describes the failure.
+ *
+ * Reference interfaces replaced (Starkdoorstep12/flashinfer-repo):
+ *   dsa_attn_fwd          solution/triton/kernel.py:138-182   kernel()
+ *                         solution/triton/kernel.py:496-567   kernel_splitk()
+ *                         solution/triton/kernel.py:707-799   kernel_splitk_v2()
+ *                         (its split partial kernel.py:343-434 and merges
+ *                         kernel.py:437-493, 583-704 run inside this call)
+ *   dsa_indexer_topk      solution/triton/indexer_kernel.py:345-433
+ *                         run_indexer_and_topk() (score kernel :4-287, top-k
+ *                         kernel :289-343)
+ *   dsa_attn_workspace_bytes / dsa_indexer_workspace_bytes
+ *                         replace the per-call torch.zeros scratch of
+ *                         kernel.py:526-528 and indexer_kernel.py:376-378
+ *                         with a caller-owned workspace.
+ */
+#ifndef DSA_ABI_H
+#define DSA_ABI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DSA_ABI_VERSION 1
+
+#define DSA_OK 0
+#define DSA_EINVAL 1      /* bad pointer, size, stride or alignment */
+#define DSA_EUNSUPPORTED 2 /* shape outside what the kernels implement */
+#define DSA_ELAUNCH 3     /* HIP launch failure */
+#define DSA_EWORKSPACE 4  /* workspace missing or too small */
+
+/*
+ * Sparse MLA attention over top-k selected cache slots
+ * (kernel.py:138-143 tensor contract; golden semantics
+ * indexer_kernel.py:436-497).
+ *
+ *   q_nope [T,H,head_dim_ckv] bf16, q_pe [T,H,head_dim_kpe] bf16
+ *   ckv    [num_pages,page_size,head_dim_ckv] bf16
+ *   kpe    [num_pages,page_size,head_dim_kpe] bf16
+ *   sparse_indices [T,topk] int32: slot id = page*page_size + offset;
+ *            -1 (and any id outside [0, num_pages*page_size)) is padding
+ *   output [T,H,head_dim_ckv] bf16, lse [T,H] fp32 (base 2; -inf and a zero
+ *            output row for a token with no valid slot)
+ *
+ * Strides are in elements; the last dimension of every tensor is contiguous
+ * and rows must be 16-byte aligned.  head_dim_ckv must be 512, head_dim_kpe
+ * 64 and H a multiple of 16.  num_splits: 0 = automatic (fills the GPU),
+ * otherwise the number of top-k chunks computed in parallel per token and
+ * merged with log-sum-exp weights.  Split results are deterministic (no
+ * atomics).
+ */
+typedef struct dsa_attn_args {
+  const void *q_nope;
+  int64_t q_nope_stride_t, q_nope_stride_h;
+  const void *q_pe;
+  int64_t q_pe_stride_t, q_pe_stride_h;
+  const void *ckv;
+  int64_t ckv_stride_page, ckv_stride_tok;
+  const void *kpe;
+  int64_t kpe_stride_page, kpe_stride_tok;
+  const int32_t *sparse_indices;
+  int64_t idx_stride_t;
+  void *output;
+  int64_t out_stride_t, out_stride_h;
+  float *lse;
+  int64_t lse_stride_t, lse_stride_h;
+  int64_t num_tokens, num_heads, topk;
+  int64_t page_size, num_pages;
+  int64_t head_dim_ckv, head_dim_kpe;
+  float sm_scale;
+  int32_t num_splits;
+  void *workspace;
+  size_t workspace_bytes;
+} dsa_attn_args;
+
+int dsa_attn_fwd(const dsa_attn_args *args, void *stream);
+
+/* Split count dsa_attn_fwd will use for this shape (requested 0 = auto). */
+int32_t dsa_attn_num_splits(int64_t num_tokens, int64_t num_heads, int64_t topk,
+                            int32_t requested);
+
+/* Workspace dsa_attn_fwd needs (0 when one split suffices). */
+size_t dsa_attn_workspace_bytes(int64_t num_tokens, int64_t num_heads, int64_t topk,
+                                int32_t requested_splits);
+
+/*
+ * Lightning indexer + top-k (indexer_kernel.py:345-433 interface; score
+ * structure :185-275; selection as :289-343 intends):
+ *
+ *   score[t,s] = sum_h w[t,h] * relu(q[t,h,:] . k[s,:] * k_scale[s])
+ *
+ * with the exact rounding order: d = exact dot of the e4m3 codes;
+ * a = fl32(fl32(d) * k_scale[s]); r = max(a, 0); v = fl32(w[t,h] * r); the
+ * head sum adds blocks of 16 heads in order, each block as
+ * (G0 + G1) + (G2 + G3), G = ((v0 + v1) + v2) + v3 over 4 consecutive heads.
+ * Position s is a candidate for row t iff s <= causal_limit[t].  The k
+ * largest candidates are selected, ties to the lower position; rows with
+ * fewer candidates are padded with -1.  Output order is ascending position.
+ * If block_table is non-NULL the output holds physical slots
+ * block_table[t*block_table_stride + s/page_size]*page_size + s%page_size.
+ *
+ *   q_idx [T,num_heads,head_dim] e4m3fn codes, k_idx [S,head_dim] e4m3fn
+ *   codes, k_scale [S] fp32, weights [T,num_heads] fp32, causal_limit [T]
+ *   int32, out [T,topk] int32; scores_out [T,S] fp32 optional (NULL = skip;
+ *   masked entries hold -inf).
+ * head_dim must be 128, num_heads a multiple of 16, topk <= 4096.
+ */
+typedef struct dsa_indexer_args {
+  const uint8_t *q_idx;
+  const uint8_t *k_idx;
+  const float *k_scale;
+  const float *weights;
+  const int32_t *causal_limit;
+  int64_t num_tokens, num_heads, head_dim, num_positions, topk;
+  const int32_t *block_table;
+  int64_t block_table_stride, page_size;
+  int32_t *out;
+  float *scores_out;
+  void *workspace;
+  size_t workspace_bytes;
+} dsa_indexer_args;
+
+int dsa_indexer_topk(const dsa_indexer_args *args, void *stream);
+
+size_t dsa_indexer_workspace_bytes(int64_t num_tokens, int64_t num_heads, int64_t head_dim,
+                                   int64_t num_positions);
+
+/* Thread-local description of the last failure ("" if none). */
+const char *dsa_last_error(void);
+
+int dsa_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSA_ABI_H */

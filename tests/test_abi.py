@@ -1,0 +1,149 @@
+"""C-ABI and host-logic tests that run without a GPU.
+
+They load libdsa_amd.so, check it exports every function include/dsa_abi.h
+declares, and exercise the host-side validation paths, which all return
+before anything is launched.
+"""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+import torch
+
+from dsa_amd import _lib, workloads
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "dsa_abi.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dsa_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_functions_are_exported():
+    lib = _lib.load()
+    declared = _declared_functions()
+    assert declared, "no declarations parsed from dsa_abi.h"
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in dsa_abi.h but not exported"
+    assert set(declared) == set(_lib.EXPORTED_SYMBOLS)
+
+
+def test_abi_version_and_struct_layout(tmp_path):
+    """The ctypes mirrors match the C structs field by field (gcc offsetof)."""
+    lib = _lib.load()
+    assert lib.dsa_abi_version() == 1
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "dsa_abi.h"', 'int main(void){']
+    for cname, cls in (("dsa_attn_args", _lib.AttnArgs), ("dsa_indexer_args", _lib.IndexerArgs)):
+        lines.append(f'printf("{cname} %zu\\n", sizeof({cname}));')
+        for f, _ in cls._fields_:
+            lines.append(f'printf("{cname}.{f} %zu\\n", offsetof({cname}, {f}));')
+    lines.append("return 0;}")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.check_call(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)])
+    got = dict(l.split() for l in subprocess.check_output([str(exe)], text=True).splitlines())
+    for cname, cls in (("dsa_attn_args", _lib.AttnArgs), ("dsa_indexer_args", _lib.IndexerArgs)):
+        assert int(got[cname]) == ctypes.sizeof(cls)
+        for f, _ in cls._fields_:
+            assert int(got[f"{cname}.{f}"]) == getattr(cls, f).offset, f
+
+
+def test_split_choice():
+    lib = _lib.load()
+    assert lib.dsa_attn_num_splits(64, 16, 2048, 0) == 4       # decode fills 256 CUs
+    assert lib.dsa_attn_num_splits(2048, 16, 2048, 0) == 1     # prefill needs no split
+    assert lib.dsa_attn_num_splits(256, 128, 2048, 0) == 1
+    assert lib.dsa_attn_num_splits(1, 16, 2048, 0) == 16       # >= one tile per wave
+    assert lib.dsa_attn_num_splits(64, 16, 2048, 16) == 16     # explicit request honoured
+    assert lib.dsa_attn_num_splits(1, 16, 5, 128) == 5         # at most one key per split
+    assert lib.dsa_attn_num_splits(4, 16, 0, 0) == 1
+    assert lib.dsa_attn_workspace_bytes(64, 16, 2048, 0) == 64 * 4 * 16 * (512 + 2) * 4
+    assert lib.dsa_attn_workspace_bytes(2048, 16, 2048, 0) == 0
+
+
+def _args(**kw):
+    a = _lib.AttnArgs()
+    base = dict(q_nope=0x1000, q_nope_stride_t=16 * 512, q_nope_stride_h=512,
+                q_pe=0x2000, q_pe_stride_t=16 * 64, q_pe_stride_h=64,
+                ckv=0x3000, ckv_stride_page=64 * 512, ckv_stride_tok=512,
+                kpe=0x4000, kpe_stride_page=64 * 64, kpe_stride_tok=64,
+                sparse_indices=0x5000, idx_stride_t=2048,
+                output=0x6000, out_stride_t=16 * 512, out_stride_h=512,
+                lse=0x7000, lse_stride_t=16, lse_stride_h=1,
+                num_tokens=64, num_heads=16, topk=2048, page_size=64, num_pages=2048,
+                head_dim_ckv=512, head_dim_kpe=64, sm_scale=0.07, num_splits=0,
+                workspace=None, workspace_bytes=0)
+    base.update(kw)
+    for k, v in base.items():
+        setattr(a, k, v)
+    return a
+
+
+def _call(a):
+    lib = _lib.load()
+    rc = lib.dsa_attn_fwd(ctypes.byref(a), None)
+    return rc, lib.dsa_last_error().decode()
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(head_dim_ckv=256), _lib.DSA_EUNSUPPORTED, "head dims"),
+    (dict(num_heads=8), _lib.DSA_EUNSUPPORTED, "multiple of 16"),
+    (dict(num_heads=0), _lib.DSA_EINVAL, "negative or zero"),
+    (dict(page_size=0), _lib.DSA_EINVAL, "negative or zero"),
+    (dict(num_splits=-1), _lib.DSA_EINVAL, "num_splits"),
+    (dict(q_nope=None), _lib.DSA_EINVAL, "NULL"),
+    (dict(ckv=0x3008), _lib.DSA_EINVAL, "16-byte"),
+    (dict(q_nope_stride_h=500), _lib.DSA_EINVAL, "16-byte"),
+    (dict(output=0x6002), _lib.DSA_EINVAL, "8-byte"),
+    (dict(), _lib.DSA_EWORKSPACE, "workspace"),            # decode needs 4 splits
+    (dict(num_splits=2, workspace=0x8000, workspace_bytes=16), _lib.DSA_EWORKSPACE, "workspace"),
+])
+def test_host_validation_rejects_before_launch(kw, code, needle):
+    rc, msg = _call(_args(**kw))
+    assert rc == code and needle in msg
+
+
+def test_zero_tokens_is_a_no_op():
+    rc, msg = _call(_args(num_tokens=0, q_nope=None))
+    assert rc == _lib.DSA_OK and msg == ""
+
+
+def test_null_args():
+    lib = _lib.load()
+    assert lib.dsa_attn_fwd(None, None) == _lib.DSA_EINVAL
+
+
+def test_shim_rejects_cpu_tensors_and_bad_shapes():
+    from dsa_amd import kernel
+    d = workloads.cfg1()
+    with pytest.raises(ValueError, match="GPU"):
+        kernel(d["q_nope"], d["q_pe"], d["ckv_cache"], d["kpe_cache"], d["sparse_indices"],
+               d["sm_scale"])
+    with pytest.raises(ValueError, match="int32"):
+        kernel(d["q_nope"], d["q_pe"], d["ckv_cache"], d["kpe_cache"],
+               d["sparse_indices"].long(), d["sm_scale"])
+    with pytest.raises(ValueError, match="multiple of 16"):
+        kernel(d["q_nope"][:, :8], d["q_pe"][:, :8], d["ckv_cache"], d["kpe_cache"],
+               d["sparse_indices"], d["sm_scale"])
+
+
+def test_workload_generators_shapes_and_padding():
+    d = workloads.cfg1()
+    assert d["sparse_indices"].shape == (4, 256) and (d["sparse_indices"][3, 200:] == -1).all()
+    assert (d["sparse_indices"][:3] >= 0).all()
+    for row in d["sparse_indices"][:3]:
+        assert row.unique().numel() == 256
+    assert workloads.attention_bytes(d["sparse_indices"]) == (3 * 256 + 200) * 1152
+    bt = torch.tensor([3, 0, 2, 1], dtype=torch.int32)
+    pos = torch.tensor([[0, 5, 64, 130, -1]])
+    assert workloads.positions_to_slots(pos, bt, 64).tolist() == [[192, 197, 0, 130, -1]]
+    sel = workloads._distinct_below(1 << 17, 2048, torch.Generator().manual_seed(0))
+    assert sel.unique().numel() == 2048 and int(sel.max()) < (1 << 17)
+    assert np.isclose(workloads.SM_SCALE, 1 / np.sqrt(192))
