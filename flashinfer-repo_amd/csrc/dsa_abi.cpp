@@ -37,9 +37,10 @@ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Top-k chunk length per split and the split count that results.  Automatic
 // mode aims for about one workgroup per compute unit while keeping at least
-// one 32-key tile per wave; an explicit request is honoured up to one key per
-// split (the reference's kernel_splitk additionally required topk % SPLIT_K
-// == 0, kernel.py:512; uneven chunks are fine here).
+// four 32-key tiles per chunk; an explicit request is honoured up to one key
+// per split (the reference's kernel_splitk additionally required topk %
+// SPLIT_K == 0, kernel.py:512; uneven chunks are fine here).  Either way a
+// chunk never exceeds kMaxChunk entries, so very long rows get extra splits.
 void choose_splits(int64_t T, int64_t H, int64_t K, int32_t requested, int32_t *splits,
                    int32_t *chunk) {
   if (K <= 0) {
@@ -49,15 +50,20 @@ void choose_splits(int64_t T, int64_t H, int64_t K, int32_t requested, int32_t *
   }
   int64_t S;
   int64_t c;
+  const int64_t min_s = ceil_div(K, dsa::kMaxChunk);
   if (requested > 0) {
     S = requested < K ? requested : K;
+    if (S < min_s) S = min_s;
     c = ceil_div(K, S);
   } else {
-    const int64_t units = (T > 0 ? T : 1) * (H / dsa::kHeadsPerGroup > 0 ? H / dsa::kHeadsPerGroup : 1);
+    // one workgroup covers up to 8 head groups (128 heads)
+    const int64_t groups = H / dsa::kHeadsPerGroup > 0 ? H / dsa::kHeadsPerGroup : 1;
+    const int64_t units = (T > 0 ? T : 1) * ceil_div(groups, 8);
     const int64_t tiles = ceil_div(K, dsa::kKeysPerTile);
-    const int64_t max_s = ceil_div(tiles, dsa::kAttnWaves);
+    const int64_t max_s = ceil_div(tiles, dsa::kMinTilesPerSplit);
     S = ceil_div(dsa::kNumCU, units);
     if (S > max_s) S = max_s;
+    if (S < min_s) S = min_s;
     if (S < 1) S = 1;
     c = ceil_div(tiles, S) * dsa::kKeysPerTile;
   }
@@ -113,7 +119,7 @@ int dsa_attn_fwd(const dsa_attn_args *a, void *stream) {
     return fail(DSA_EUNSUPPORTED, "dsa_attn_fwd: size beyond the supported range");
   if (a->num_splits < 0) return fail(DSA_EINVAL, "dsa_attn_fwd: num_splits must be >= 0");
   if (a->num_tokens == 0) return ok();
-  if (!a->q_nope || !a->q_pe || !a->sparse_indices || !a->output || !a->lse)
+  if (!a->q_nope || !a->q_pe || !a->output || !a->lse || (a->topk > 0 && !a->sparse_indices))
     return fail(DSA_EINVAL, "dsa_attn_fwd: NULL tensor pointer");
   if (a->num_pages > 0 && (!a->ckv || !a->kpe))
     return fail(DSA_EINVAL, "dsa_attn_fwd: NULL cache pointer");

@@ -10,20 +10,30 @@
 //
 // over the valid slots s_j of sparse_indices[t] (-1 = padding).
 //
-// Work decomposition.  One workgroup = one (token, top-k chunk, 16-head
-// group) with four independent waves.  Each wave walks its own 32-key tiles
-// of the chunk: it gathers the 32 selected rows (1024 B ckv + 128 B kpe each)
-// with global_load_lds_dwordx4 straight into a private LDS tile (no VGPR
-// staging, 36 row loads in flight per wave), then
-//   S^T[32 keys x 16 heads] = K[keys x 576] . Q^T          (bf16 MFMA 16x16x32)
-//   online softmax in fp32 (log2 domain)
-//   O^T[512 x 16 heads]    += V^T[512 x 32 keys] . P^T      (bf16 MFMA 16x16x32)
-// Computing S^T (keys as the MFMA M dimension) leaves P^T in exactly the
-// lane layout the PV product takes as its B operand, so P never round-trips
-// through LDS.  At the end the four waves' (m, l, O) states are merged in LDS
-// and the workgroup writes either the final bf16 output and lse (one chunk per
-// token) or an unnormalised fp32 partial that dsa_attn_combine merges with
-// log-sum-exp weights (reference merge algebra: kernel.py:461-493).
+// Work decomposition.  One workgroup = one (token, top-k chunk, block of
+// head groups).  Its waves share a 3-stage LDS ring of 32-key tiles: every
+// tile is gathered with global_load_lds_dwordx4 (16 B per lane straight into
+// LDS, no VGPR staging; one 1 KB ckv row per instruction, 8 kpe rows per
+// instruction), two tiles in flight while the third is consumed.  The chunk's
+// slot ids are staged in LDS once, so issuing a tile's gathers never waits on
+// an index load.  Padding keys gather a zero row, which keeps the number of
+// loads per wave and tile fixed and makes the vmcnt-based stage waits exact.
+//
+// Each wave belongs to one 16-head group and owns one slice of the 512 output
+// features.  Per tile:
+//   S^T[32 keys x 16 heads] = K[keys x 576] . Q^T       (bf16 MFMA 16x16x32)
+//     -- when FS > 1 waves share a head group, they split the 2 key blocks x
+//        18 k-steps of this product and add the partial S^T through LDS in a
+//        fixed order, so every wave of the group holds identical scores;
+//   online softmax in fp32 (log2 domain);
+//   O^T[slice x 16 heads] += V^T[slice x 32 keys] . P^T  (bf16 MFMA 16x16x32,
+//     P split into bf16 hi + lo parts, ~16-bit P; the V^T operand is read
+//     with ds_read_b64_tr_b16, which transposes 16-bit elements across lanes).
+// Computing S^T (keys as the MFMA M dimension) leaves P^T in exactly the lane
+// layout the PV product takes as its B operand.  A workgroup writes either the
+// final bf16 output and lse (one chunk per token) or an unnormalised fp32
+// partial that dsa_attn_combine_kernel merges with log-sum-exp weights
+// (reference merge algebra: kernel.py:461-493).
 //
 // MFMA 16x16x32 bf16 lane layout used throughout (lane = 16*g + r):
 //   A (16 x 32): lane holds row r, k-slots 8g..8g+7
@@ -31,55 +41,90 @@
 //   D (16 x 16): lane holds column r, rows 4g..4g+3
 // Only the A/B k-slot assignment being identical matters for a product, so
 // the kernel assigns k-slots to features or keys as convenient.
+//
+// ds_read_b64_tr_b16, per 16-lane group: lane i receives element i%4 of the
+// 4-element (8-byte) rows addressed by lanes 4j + i/4, j = 0..3.  Pointing
+// lanes 4j..4j+3 at 8-byte pieces f0..f0+15 of key row j gives lane i the
+// feature f0+i of keys 0..3: one half of an A operand of V^T.
 #include "dsa_internal.h"
 
 namespace dsa {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
-typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
 
-// LDS tile geometry (bytes).  A ckv row is padded from 1024 to 1040 B so the
-// 16 rows one MFMA operand read touches fall in distinct banks; kpe rows are
-// gathered 8 per DMA instruction in chunk-major order (lane i of the DMA
-// holds 16-byte chunk i/8 of row i%8), so a column read of 16 rows hits 16
+// LDS geometry (bytes).  A ckv row is padded from 1024 to 1040 B so the 16
+// rows one MFMA operand read touches fall in distinct banks; kpe rows are
+// gathered 8 per DMA instruction in chunk-major order (lane i of the DMA holds
+// 16-byte chunk i/8 of row i%8), so a column read of 16 rows hits 16
 // consecutive chunks.
 constexpr int kCkvPitch = 1024 + 16;
 constexpr int kKpeGroupPitch = 1024 + 128;
-constexpr int kCkvTileBytes = kKeysPerTile * kCkvPitch;
-constexpr int kKpeTileBytes = (kKeysPerTile / 8) * kKpeGroupPitch;
-constexpr int kWaveTileBytes = kCkvTileBytes + kKpeTileBytes;
-constexpr int kLdsBytes = kAttnWaves * kWaveTileBytes;
-constexpr int kMergeBytes = kAttnWaves * 32 * 64 * 16;
-static_assert(kMergeBytes <= kLdsBytes, "merge buffer must fit in the tile buffers");
-static_assert(kLdsBytes + 2 * kAttnWaves * 16 * 4 <= 160 * 1024, "LDS budget of one gfx950 CU");
+constexpr int kCkvStageBytes = kKeysPerTile * kCkvPitch;
+constexpr int kStageBytes = kCkvStageBytes + (kKeysPerTile / 8) * kKpeGroupPitch;
+constexpr int kStages = 3;
+constexpr int kIdxBytes = kMaxChunk * 4;
+constexpr int kXchgBytes = 8 * 64 * 16;  // one f32x4 per lane per wave
+constexpr int kLdsBytes = kStages * kStageBytes + kIdxBytes + kXchgBytes;
+static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one gfx950 CU");
+
+// Padding keys gather from here (global memory, never written).
+__device__ __attribute__((aligned(64))) const uint4 g_zero_row[64] = {};
 
 __device__ __forceinline__ void lds_dma16(const void *gsrc, void *ldst) {
   __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)gsrc,
                                    (__attribute__((address_space(3))) void *)ldst, 16, 0, 0);
 }
 
-__device__ __forceinline__ int64_t readlane64(int64_t v, int lane) {
+__device__ __forceinline__ bf16x4 lds_read_tr16(const char *p) {
+  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) i16x4 *)(p));
+  return __builtin_bit_cast(bf16x4, v);
+}
+
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int lane) {
   const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, lane);
-  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)v >> 32), lane);
-  return (int64_t)(((uint64_t)hi << 32) | lo);
+  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), lane);
+  return ((uint64_t)hi << 32) | lo;
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-__device__ __forceinline__ unsigned short f32_to_bf16_rne(float f) {
-  uint32_t u = __builtin_bit_cast(uint32_t, f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (unsigned short)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (unsigned short)(u >> 16);
+// Waits until at most N of this wave's vector-memory operations are
+// outstanding (they complete in issue order).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-__global__ __launch_bounds__(kAttnWaves * 64, 1) void dsa_attn_partial_kernel(AttnParams p) {
+// W waves per workgroup; FS waves share one 16-head group, each owning
+// 512/FS output features.  W/FS head groups per workgroup.  With FS > 1 the
+// waves of a group split S^T = K Q^T: 2 key blocks x kParts step ranges.
+template <int W, int FS>
+struct Ring {
+  static constexpr int kHG = W / FS;
+  static constexpr int kNFB = 32 / FS;            // 16-feature blocks per wave
+  static constexpr int kRows = kKeysPerTile / W;  // ckv rows one wave gathers per tile
+  static constexpr int kLoads = kRows + 1;        // + one kpe DMA (full or half)
+  static constexpr int kParts = FS >= 2 ? FS / 2 : 1;              // k-step ranges per block
+  static constexpr int kBlocks = FS >= 2 ? 1 : 2;                  // key blocks one wave computes
+  static constexpr int kSteps = 18 / kParts;                       // k-steps per range
+  static_assert(W == 4 || W == 8, "gather split assumes 4 or 8 waves");
+  static_assert(FS == 1 || FS == 2 || FS == 4, "feature slices");
+  static_assert(18 % kParts == 0, "k-step split");
+};
+
+template <int W, int FS>
+__global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) {
+  using R = Ring<W, FS>;
   __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
-  __shared__ float lds_m[kAttnWaves][16];
-  __shared__ float lds_l[kAttnWaves][16];
+  int32_t *lds_idx = (int32_t *)(lds + kStages * kStageBytes);
+  f32x4 *xbuf = (f32x4 *)(lds + kStages * kStageBytes + kIdxBytes);
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -87,106 +132,144 @@ __global__ __launch_bounds__(kAttnWaves * 64, 1) void dsa_attn_partial_kernel(At
   const int split = blockIdx.x - t * p.num_splits;
   const int r16 = lane & 15;
   const int g = lane >> 4;
-  const int head = blockIdx.y * kHeadsPerGroup + r16;
+  const int hg = wave / FS;
+  const int fs = wave - hg * FS;
+  const int head = (blockIdx.y * R::kHG + hg) * kHeadsPerGroup + r16;
+  // this wave's share of S^T: key block qb0 (+1 if kBlocks == 2), steps s0..
+  const int qb0 = FS >= 2 ? (fs & 1) : 0;
+  const int s0 = FS >= 2 ? (fs >> 1) * R::kSteps : 0;
 
   const int k_begin = split * p.chunk;
-  const int k_end = min(p.K, k_begin + p.chunk);
-  const int n_keys = max(0, k_end - k_begin);
+  const int n_keys = max(0, min(p.K, k_begin + p.chunk) - k_begin);
   const int n_tiles = (n_keys + kKeysPerTile - 1) / kKeysPerTile;
 
-  // Q^T as the B operand of S^T = K Q^T: k-step s covers features 32s..32s+31
-  // (s < 16: q_nope; s = 16, 17: q_pe), this lane holds 8g..8g+7 of them.
-  bf16x8 qreg[18];
+  // ---- stage the chunk's slot ids (invalid -> -1), padded to whole tiles;
+  // all loads are issued before the first store so they overlap
   {
-    const char *qn = p.q_nope + t * p.qn_st + head * p.qn_sh + g * 16;
+    constexpr int kPer = kMaxChunk / (W * 64);
+    const int32_t *src = p.idx + (int64_t)t * p.idx_st + k_begin;
+    int sv[kPer];
 #pragma unroll
-    for (int s = 0; s < 16; ++s) qreg[s] = *(const bf16x8 *)(qn + s * 64);
-    const char *qp = p.q_pe + t * p.qp_st + head * p.qp_sh + g * 16;
+    for (int k = 0; k < kPer; ++k) {
+      const int i = threadIdx.x + k * W * 64;
+      sv[k] = i < n_keys ? src[i] : -1;
+    }
 #pragma unroll
-    for (int s = 0; s < 2; ++s) qreg[16 + s] = *(const bf16x8 *)(qp + s * 64);
+    for (int k = 0; k < kPer; ++k) {
+      const int i = threadIdx.x + k * W * 64;
+      const int s = sv[k];
+      if (i < n_tiles * kKeysPerTile) lds_idx[i] = (s < 0 || (int64_t)s >= p.num_slots) ? -1 : s;
+    }
   }
 
-  f32x4 acc[32];
+  // Q^T as the B operand of S^T = K Q^T: k-step s covers features 32s..32s+31
+  // (s < 16: q_nope; s = 16, 17: q_pe); this lane holds 8g..8g+7 of them.
+  bf16x8 qreg[R::kSteps];
+  {
+    const char *qn = p.q_nope + t * p.qn_st + head * p.qn_sh + g * 16;
+    const char *qp = p.q_pe + t * p.qp_st + head * p.qp_sh + g * 16;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY;  // running max of x*log2(e), this lane's head
+    for (int k = 0; k < R::kSteps; ++k) {
+      const int s = s0 + k;
+      qreg[k] = *(const bf16x8 *)(s < 16 ? qn + s * 64 : qp + (s - 16) * 64);
+    }
+  }
+  // Retire the Q loads with a wait the compiler sees (s_waitcnt vmcnt(0)), so
+  // its own bookkeeping has nothing outstanding when the gather ring starts
+  // and it adds no drain at the loop header.
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __syncthreads();  // slot ids visible; nothing gathered yet
+
+  // ---- gather issue: this wave's share of tile j into stage j % kStages.
+  // Lane l owns the slot of key 8*grp + (l & 7) of the tile, grp being the
+  // kpe group (8 rows) this wave gathers (a half group when W == 8).
+  const int grp = (W == 4) ? wave : (wave >> 1);
+  const int row0 = (W == 4) ? 0 : 4 * (wave & 1);  // first ckv row within the group
+  auto issue_tile = [&](int j) {
+    char *st = lds + (j % kStages) * kStageBytes;
+    const int s = lds_idx[j * kKeysPerTile + grp * 8 + (lane & 7)];
+    uint64_t ckv_addr = (uint64_t)(const char *)g_zero_row;
+    uint64_t kpe_addr = ckv_addr;
+    if (s >= 0) {
+      const uint32_t pg = (uint32_t)s / (uint32_t)p.page_size;
+      const uint32_t of = (uint32_t)s - pg * (uint32_t)p.page_size;
+      ckv_addr = (uint64_t)(p.ckv + (int64_t)pg * p.ckv_sp + (int64_t)of * p.ckv_so);
+      kpe_addr = (uint64_t)(p.kpe + (int64_t)pg * p.kpe_sp + (int64_t)of * p.kpe_so);
+    }
+#pragma unroll
+    for (int m = 0; m < R::kRows; ++m) {
+      const int key = grp * 8 + row0 + m;
+      const char *src = (const char *)readlane64(ckv_addr, row0 + m) + lane * 16;
+      lds_dma16(src, st + key * kCkvPitch);
+    }
+    char *kdst = st + kCkvStageBytes + grp * kKpeGroupPitch;
+    const char *ksrc = (const char *)kpe_addr + (lane >> 3) * 16;
+    if (W == 4 || (lane >> 5) == (wave & 1)) lds_dma16(ksrc, kdst);
+  };
+
+  f32x4 acc[R::kNFB];
+#pragma unroll
+  for (int i = 0; i < R::kNFB; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY;  // running max of x*log2(e) for this lane's head
   float l_run = 0.f;        // running sum over this lane's keys (reduced at the end)
 
-  char *tile_ckv = lds + wave * kWaveTileBytes;
-  char *tile_kpe = tile_ckv + kCkvTileBytes;
-  const int32_t *idx_row = p.idx + (int64_t)t * p.idx_st;
+  const int pre = min(n_tiles, kStages - 1);
+  for (int j = 0; j < pre; ++j) issue_tile(j);
 
-  for (int tile = wave; tile < n_tiles; tile += kAttnWaves) {
-    const int kb = k_begin + tile * kKeysPerTile;
-    const int nk = min(kKeysPerTile, k_end - kb);
+  for (int i = 0; i < n_tiles; ++i) {
+    if (i + 1 < n_tiles)
+      wait_vmcnt<R::kLoads>();  // tile i+1 may stay in flight
+    else
+      wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();  // every wave's share of tile i landed; tile i-1 consumed
+    if (i + kStages - 1 < n_tiles) issue_tile(i + kStages - 1);
 
-    // ---- slot ids of this tile's keys (lane & 31) and their row offsets
-    int slot = -1;
-    if ((lane & 31) < nk) slot = idx_row[kb + (lane & 31)];
-    const bool valid = slot >= 0 && (int64_t)slot < p.num_slots;
-    const uint32_t vmask = (uint32_t)__ballot(valid);
-    int64_t ckv_off = 0, kpe_off = 0;
-    if (valid) {
-      const uint32_t pg = (uint32_t)slot / (uint32_t)p.page_size;
-      const uint32_t of = (uint32_t)slot - pg * (uint32_t)p.page_size;
-      ckv_off = (int64_t)pg * p.ckv_sp + (int64_t)of * p.ckv_so;
-      kpe_off = (int64_t)pg * p.kpe_sp + (int64_t)of * p.kpe_so;
-    }
+    const char *st_ckv = lds + (i % kStages) * kStageBytes;
+    const char *st_kpe = st_ckv + kCkvStageBytes;
+    const uint32_t vmask = (uint32_t)__ballot(lds_idx[i * kKeysPerTile + (lane & 31)] >= 0);
 
-    // ---- gather: 32 ckv rows (one 1 KB DMA each) + 4 x 8 kpe rows.
-    // Invalid or missing keys get a zero row so padding never feeds NaN/Inf
-    // garbage into the MFMAs (their probabilities are exactly zero).
-#pragma unroll
-    for (int r = 0; r < kKeysPerTile; ++r) {
-      char *dst = tile_ckv + r * kCkvPitch;
-      if ((vmask >> r) & 1u) {
-        lds_dma16(p.ckv + readlane64(ckv_off, r) + lane * 16, dst);
-      } else {
-        *(uint4 *)(dst + lane * 16) = make_uint4(0u, 0u, 0u, 0u);
-      }
-    }
-#pragma unroll
-    for (int q = 0; q < kKeysPerTile / 8; ++q) {
-      const int r = q * 8 + (lane & 7);
-      const int64_t off = __shfl(kpe_off, r);
-      char *dst = tile_kpe + q * kKpeGroupPitch;
-      if ((vmask >> r) & 1u) {
-        lds_dma16(p.kpe + off + (lane >> 3) * 16, dst);
-      } else {
-        *(uint4 *)(dst + lane * 16) = make_uint4(0u, 0u, 0u, 0u);
-      }
-    }
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-
-    // ---- S^T = K . Q^T for two 16-key blocks
+    // ---- S^T = K . Q^T (this wave's blocks and k-steps)
     f32x4 sacc[2];
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
+    for (int bb = 0; bb < R::kBlocks; ++bb) {
+      const int b = qb0 + bb;
       f32x4 c = {0.f, 0.f, 0.f, 0.f};
-      const char *rowp = tile_ckv + (b * 16 + r16) * kCkvPitch + g * 16;
-#pragma unroll
-      for (int s = 0; s < 16; ++s)
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)(rowp + s * 64), qreg[s], c,
-                                                     0, 0, 0);
+      const char *rowp = st_ckv + (b * 16 + r16) * kCkvPitch + g * 16;
       const int kk = b * 16 + r16;
-      const char *kp = tile_kpe + (kk >> 3) * kKpeGroupPitch + (kk & 7) * 16;
+      const char *kp = st_kpe + (kk >> 3) * kKpeGroupPitch + (kk & 7) * 16;
 #pragma unroll
-      for (int s = 0; s < 2; ++s)
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)(kp + (s * 4 + g) * 128),
-                                                     qreg[16 + s], c, 0, 0, 0);
-      sacc[b] = c;
+      for (int k = 0; k < R::kSteps; ++k) {
+        const int s = s0 + k;
+        const char *ap = s < 16 ? rowp + s * 64 : kp + ((s - 16) * 4 + g) * 128;
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)ap, qreg[k], c, 0, 0, 0);
+      }
+      sacc[bb] = c;
+    }
+    if (FS >= 2) {
+      // partial scores of the group's waves, added in a fixed order
+      xbuf[wave * 64 + lane] = sacc[0];
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): partial written
+      __builtin_amdgcn_s_barrier();
+      const int base = hg * FS;
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        f32x4 c = xbuf[(base + b) * 64 + lane];
+#pragma unroll
+        for (int part = 1; part < R::kParts; ++part) c += xbuf[(base + b + 2 * part) * 64 + lane];
+        sacc[b] = c;
+      }
     }
 
-    // ---- online softmax (this lane: head r16, keys b*16 + 4g + i)
+    // ---- online softmax (this lane: head r16, keys b*16 + 4g + k)
     float x[8];
     float mx = -INFINITY;
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = b * 16 + 4 * g + i;
-        const float v = ((vmask >> key) & 1u) ? sacc[b][i] * p.scale_log2 : -INFINITY;
-        x[b * 4 + i] = v;
+      for (int k = 0; k < 4; ++k) {
+        const int key = b * 16 + 4 * g + k;
+        const float v = ((vmask >> key) & 1u) ? sacc[b][k] * p.scale_log2 : -INFINITY;
+        x[b * 4 + k] = v;
         mx = fmaxf(mx, v);
       }
     mx = fmaxf(mx, __shfl_xor(mx, 16));
@@ -194,88 +277,81 @@ __global__ __launch_bounds__(kAttnWaves * 64, 1) void dsa_attn_partial_kernel(At
     const float m_new = fmaxf(m_run, mx);
     const bool none = m_new == -INFINITY;
     const float alpha = none ? 1.f : fast_exp2(m_run - m_new);
-    u16x8 pbits;
+    bf16x8 p_hi, p_lo;
     float psum = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float pv = none ? 0.f : fast_exp2(x[i] - m_new);
+    for (int k = 0; k < 8; ++k) {
+      const float pv = none ? 0.f : fast_exp2(x[k] - m_new);
       psum += pv;
-      pbits[i] = f32_to_bf16_rne(pv);
+      p_hi[k] = (__bf16)pv;
+      p_lo[k] = (__bf16)(pv - (float)p_hi[k]);
     }
     l_run = l_run * alpha + psum;
     m_run = m_new;
-    const bf16x8 pB = __builtin_bit_cast(bf16x8, pbits);
 
-    // ---- O^T += V^T . P^T: k-slot i of group g is key 4g+i (i<4) or 16+4g+(i-4)
-    const char *vcol = tile_ckv + r16 * 2;
-    const char *vrow[8];
+    // ---- O^T += V^T . P^T over this wave's feature slice; k-slot k of lane
+    // group g is key 4g+k (k < 4) or 16+4g+(k-4).
+    if (FS >= 2) {
+      // Lane 16g+s points the transpose read at key row 4g + s/4 (+16),
+      // features f0 + 4*(s%4).
+      const char *vsrc = st_ckv + (4 * g + (r16 >> 2)) * kCkvPitch +
+                         (fs * R::kNFB * 16 + 4 * (r16 & 3)) * 2;
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      vrow[i] = vcol + ((i < 4) ? (4 * g + i) : (16 + 4 * g + i - 4)) * kCkvPitch;
+      for (int fb = 0; fb < R::kNFB; ++fb) {
+        const bf16x4 lo4 = lds_read_tr16(vsrc + fb * 32);
+        const bf16x4 hi4 = lds_read_tr16(vsrc + 16 * kCkvPitch + fb * 32);
+        const bf16x8 av = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+        f32x4 c = acc[fb] * alpha;
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, p_hi, c, 0, 0, 0);
+        acc[fb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, p_lo, c, 0, 0, 0);
+      }
+    } else {
+      // Full-slice waves (FS == 1) gather the V^T operand with 16-bit reads:
+      // with transpose reads the compiler hoists all 64 of them and the
+      // 8-wave variant runs out of registers.
+      const char *vcol = st_ckv + (fs * R::kNFB * 16 + r16) * 2;
+      const char *vrow[8];
 #pragma unroll
-    for (int fb = 0; fb < 32; ++fb) {
-      u16x8 a;
+      for (int k = 0; k < 8; ++k)
+        vrow[k] = vcol + ((k < 4) ? (4 * g + k) : (16 + 4 * g + k - 4)) * kCkvPitch;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) a[i] = *(const unsigned short *)(vrow[i] + fb * 32);
-      acc[fb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), pB,
-                                                        acc[fb] * alpha, 0, 0, 0);
+      for (int fb = 0; fb < R::kNFB; ++fb) {
+        u16x8 a;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) a[k] = *(const unsigned short *)(vrow[k] + fb * 32);
+        const bf16x8 av = __builtin_bit_cast(bf16x8, a);
+        f32x4 c = acc[fb] * alpha;
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, p_hi, c, 0, 0, 0);
+        acc[fb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, p_lo, c, 0, 0, 0);
+      }
     }
   }
 
-  // ---- merge the four waves' states through LDS
+  // ---- epilogue: lanes of a head hold partial sums over disjoint keys
   l_run += __shfl_xor(l_run, 16);
   l_run += __shfl_xor(l_run, 32);
-  __syncthreads();
-  f32x4 *mbuf = (f32x4 *)lds;
-#pragma unroll
-  for (int fb = 0; fb < 32; ++fb) mbuf[(wave * 32 + fb) * 64 + lane] = acc[fb];
-  if (lane < 16) {
-    lds_m[wave][lane] = m_run;
-    lds_l[wave][lane] = l_run;
-  }
-  __syncthreads();
-
-  float mw[kAttnWaves];
-  float M = -INFINITY;
-#pragma unroll
-  for (int w = 0; w < kAttnWaves; ++w) {
-    mw[w] = lds_m[w][r16];
-    M = fmaxf(M, mw[w]);
-  }
-  float aw[kAttnWaves];
-  float L = 0.f;
-#pragma unroll
-  for (int w = 0; w < kAttnWaves; ++w) {
-    aw[w] = (mw[w] == -INFINITY) ? 0.f : fast_exp2(mw[w] - M);
-    L += aw[w] * lds_l[w][r16];
-  }
-
   const bool final_out = p.num_splits == 1;
-  const float inv = (M == -INFINITY) ? 0.f : 1.f / L;
+  const float inv = (m_run == -INFINITY) ? 0.f : 1.f / l_run;
+  const int64_t prow = ((int64_t)t * p.num_splits + split) * p.H + head;
 #pragma unroll
-  for (int j = 0; j < 32 / kAttnWaves; ++j) {
-    const int fb = wave * (32 / kAttnWaves) + j;
-    f32x4 o = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) o += aw[w] * mbuf[(w * 32 + fb) * 64 + lane];
-    const int f0 = fb * 16 + 4 * g;
+  for (int fb = 0; fb < R::kNFB; ++fb) {
+    const int f0 = (fs * R::kNFB + fb) * 16 + 4 * g;
     if (final_out) {
-      u16x4 ob;
+      bf16x4 ob;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) ob[i] = f32_to_bf16_rne(o[i] * inv);
-      *(u16x4 *)(p.out + t * p.out_st + head * p.out_sh + f0 * 2) = ob;
+      for (int k = 0; k < 4; ++k) ob[k] = (__bf16)(acc[fb][k] * inv);
+      *(bf16x4 *)(p.out + t * p.out_st + head * p.out_sh + f0 * 2) = ob;
     } else {
-      const int64_t row = ((int64_t)t * p.num_splits + split) * p.H + head;
-      *(f32x4 *)(p.part_acc + row * kHeadDimCkv + f0) = o;
+      *(f32x4 *)(p.part_acc + prow * kHeadDimCkv + f0) = acc[fb];
     }
   }
-  if (wave == 0 && lane < 16) {
+  if (fs == 0 && lane < 16) {
     if (final_out) {
-      p.lse[t * p.lse_st + head * p.lse_sh] = (M == -INFINITY) ? -INFINITY : M + __log2f(L);
+      p.lse[t * p.lse_st + head * p.lse_sh] =
+          (m_run == -INFINITY) ? -INFINITY : m_run + __log2f(l_run);
     } else {
-      const int64_t row = ((int64_t)t * p.num_splits + split) * p.H + head;
-      p.part_ml[row * 2 + 0] = M;
-      p.part_ml[row * 2 + 1] = L;
+      p.part_ml[prow * 2 + 0] = m_run;
+      p.part_ml[prow * 2 + 1] = l_run;
     }
   }
 }
@@ -302,10 +378,10 @@ __global__ __launch_bounds__(128) void dsa_attn_combine_kernel(AttnParams p) {
     o += a * *(const f32x4 *)(p.part_acc + row * kHeadDimCkv + f0);
   }
   const float inv = (M == -INFINITY) ? 0.f : 1.f / L;
-  u16x4 ob;
+  bf16x4 ob;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) ob[i] = f32_to_bf16_rne(o[i] * inv);
-  *(u16x4 *)(p.out + t * p.out_st + head * p.out_sh + f0 * 2) = ob;
+  for (int i = 0; i < 4; ++i) ob[i] = (__bf16)(o[i] * inv);
+  *(bf16x4 *)(p.out + t * p.out_st + head * p.out_sh + f0 * 2) = ob;
   if (threadIdx.x == 0)
     p.lse[t * p.lse_st + head * p.lse_sh] = (M == -INFINITY) ? -INFINITY : M + __log2f(L);
 }
@@ -314,8 +390,21 @@ __global__ __launch_bounds__(128) void dsa_attn_combine_kernel(AttnParams p) {
 
 hipError_t launch_attention(const AttnParams &p, hipStream_t stream) {
   if (p.T == 0) return hipSuccess;
-  const dim3 grid(p.T * p.num_splits, p.H / kHeadsPerGroup);
-  hipLaunchKernelGGL(dsa_attn_partial_kernel, grid, dim3(kAttnWaves * 64), 0, stream, p);
+  const int groups = p.H / kHeadsPerGroup;
+  if (groups % 8 == 0) {
+    // 8 waves, one per 16-head group, all 512 features each
+    hipLaunchKernelGGL((dsa_attn_ring_kernel<8, 1>), dim3(p.T * p.num_splits, groups / 8),
+                       dim3(8 * 64), 0, stream, p);
+  } else if (groups % 4 == 0) {
+    hipLaunchKernelGGL((dsa_attn_ring_kernel<4, 1>), dim3(p.T * p.num_splits, groups / 4),
+                       dim3(4 * 64), 0, stream, p);
+  } else if (groups % 2 == 0) {
+    hipLaunchKernelGGL((dsa_attn_ring_kernel<4, 2>), dim3(p.T * p.num_splits, groups / 2),
+                       dim3(4 * 64), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((dsa_attn_ring_kernel<4, 4>), dim3(p.T * p.num_splits, groups),
+                       dim3(4 * 64), 0, stream, p);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.num_splits == 1) return e;
   hipLaunchKernelGGL(dsa_attn_combine_kernel, dim3(p.T, p.H), dim3(128), 0, stream, p);

@@ -15,8 +15,9 @@ constexpr int kNumCU = 256;
 constexpr int kHeadDimCkv = 512;
 constexpr int kHeadDimKpe = 64;
 constexpr int kHeadsPerGroup = 16;  // MFMA N dimension: one 16-head group
-constexpr int kKeysPerTile = 32;    // keys one wave gathers and consumes per step
-constexpr int kAttnWaves = 4;       // waves per workgroup (independent key streams)
+constexpr int kKeysPerTile = 32;       // keys gathered into one LDS ring stage
+constexpr int kMinTilesPerSplit = 4;   // automatic splits keep >= 4 tiles of work each
+constexpr int kMaxChunk = 2048;        // top-k entries one workgroup handles (LDS-staged ids)
 
 struct AttnParams {
   const char *q_nope;  // byte strides below
