@@ -6,11 +6,13 @@ A step is one call of ``dsa_amd.kernel`` (the drop-in for the reference's
 ``kernel()``, solution/triton/kernel.py:138) on the BASELINE decode workload:
 T=64 tokens, H=16, top-k=2048, ckv512+kpe64 bf16, 131072 slots in pages of 64
 (config 2).  Inputs are synthetic, seeded, and resident in HBM before timing.
-The step is captured once in a HIP graph and replayed, so the figure is the
-GPU time of the path rather than Python/ctypes launch overhead (the eager
-per-call time is reported alongside).  Timing uses HIP events on the stream
-the kernels run on: W untimed warm-up steps, then K timed steps between
-synchronisations.
+Steps are captured 20 at a time in a HIP graph and the graph is replayed, so
+the figure is the GPU time of back-to-back calls rather than Python/ctypes
+launch overhead (the eager per-call time is reported alongside).  Timing uses
+HIP events on the stream the kernels run on: W untimed warm-up steps, then K
+timed steps between synchronisations.  The dominant kernel (the per-chunk
+gather attention, without the split merge) is timed the same way on its own
+through dsa_attn_fwd_partial; its duration gives the roofline figure.
 
 Prints one JSON line (metric, value in us/call, roofline of the dominant
 kernel, and a CPU baseline: the CPU oracle timed on this host).
@@ -29,6 +31,7 @@ sys.path[:0] = [ROOT, os.path.join(ROOT, "flashinfer-repo_amd")]
 METRIC = "µs/call + HBM GB/s & MFMA %, DSA decode H=16 topk=2048 T=64"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+GRAPH_CALLS = 20
 
 
 def parse():
@@ -41,6 +44,19 @@ def parse():
                     help="budget of the CPU-oracle baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
+
+
+def load_traffic(config: str):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3
+    --pmc summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    ent = t.get(config)
+    return None if ent is None else ent.get("hbm_bytes_per_launch")
 
 
 def cpu_baseline(d, budget_s: float):
@@ -82,7 +98,7 @@ def main():
 
     import torch
 
-    from dsa_amd import kernel, num_splits, workloads
+    from dsa_amd import kernel, kernel_partial, num_splits, workloads
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -95,32 +111,49 @@ def main():
     alg_bytes = workloads.attention_bytes(d["sparse_indices"])
     alg_flops = workloads.attention_flops(d["sparse_indices"], H)
 
-    # eager warm-up, then capture one step
-    for _ in range(3):
-        kernel(*args)
-    torch.cuda.synchronize()
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        kernel(*args)
-    torch.cuda.current_stream().wait_stream(s)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        kernel(*args)
-    torch.cuda.synchronize()
+    def graph_of(fn, n):
+        """Capture n back-to-back calls of fn in one HIP graph (after an eager
+        warm-up on the capture-side stream, as torch's graph API expects)."""
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fn()
+        torch.cuda.current_stream().wait_stream(s)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(n):
+                fn()
+        torch.cuda.synchronize()
+        return graph
 
-    for _ in range(a.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(a.steps):
-        graph.replay()
-    end.record()
-    torch.cuda.synchronize()
-    ms_per_step = start.elapsed_time(end) / a.steps
+    def time_graph(graph, n_per, steps, warmup):
+        """ms per call: warm-up replays, then HIP events around the replays
+        (on the current stream, which the kernels run on)."""
+        reps = max(1, -(-steps // n_per))
+        for _ in range(max(1, -(-warmup // n_per))):
+            graph.replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / (reps * n_per), reps * n_per
+
+    per_graph = min(GRAPH_CALLS, a.steps)
+    step_graph = graph_of(lambda: kernel(*args), per_graph)
+    ms_per_step, timed_steps = time_graph(step_graph, per_graph, a.steps, a.warmup)
+
+    # the dominant kernel alone: the gather-attention launch without the merge
+    part_graph = graph_of(lambda: kernel_partial(*args, num_splits=0), per_graph)
+    ms_partial, _ = time_graph(part_graph, per_graph, a.steps, a.warmup)
 
     # eager (Python shim + ctypes + launches) for reference
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(a.steps):
         kernel(*args)
@@ -129,15 +162,16 @@ def main():
     eager_ms = start.elapsed_time(end) / a.steps
 
     us = ms_per_step * 1e3
-    gbs = alg_bytes / (ms_per_step * 1e-3) / 1e9
-    tflops = alg_flops / (ms_per_step * 1e-3) / 1e12
+    gbs = alg_bytes / (ms_partial * 1e-3) / 1e9          # dominant kernel
+    tflops = alg_flops / (ms_partial * 1e-3) / 1e12
     splits = num_splits(T, H, K)
+    traffic = load_traffic(a.config)
     line = {
         "metric": METRIC,
         "value": round(us, 3),
         "unit": "µs/call",
         "n_gpus": 1,
-        "steps": a.steps,
+        "steps": timed_steps,
         "warmup": a.warmup,
         "ms_per_step": round(ms_per_step, 6),
         "higher_is_better": False,
@@ -149,12 +183,16 @@ def main():
                                f"ckv512+kpe64 bf16, {d['ckv_cache'].numel() // 512} slots, "
                                f"page_size={d['ckv_cache'].shape[1]}",
                    "tokens": T, "heads": H, "topk": K, "splits": splits,
-                   "timing": "HIP-graph replay of one kernel() call per step",
-                   "eager_us_per_call": round(eager_ms * 1e3, 3)},
+                   "timing": f"HIP graphs of {per_graph} back-to-back kernel() calls, replayed",
+                   "eager_us_per_call": round(eager_ms * 1e3, 3),
+                   "dominant_kernel_us": round(ms_partial * 1e3, 3),
+                   "merge_and_gaps_us": round((ms_per_step - ms_partial) * 1e3, 3)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic,
                      "algorithmic_bytes": alg_bytes,
-                     "kernel": "dsa_attn_partial_kernel+dsa_attn_combine_kernel (whole step)"},
+                     "kernel": "dsa_attn_ring_kernel (per-chunk gather attention; "
+                               "timed alone via dsa_attn_fwd_partial)"},
         "mfma": {"achieved_tflops": round(tflops, 2), "peak_tflops": BF16_PEAK_TFLOPS,
                  "frac": round(tflops / BF16_PEAK_TFLOPS, 5), "algorithmic_flops": alg_flops},
     }

@@ -72,10 +72,15 @@ void choose_splits(int64_t T, int64_t H, int64_t K, int32_t requested, int32_t *
   *chunk = (int32_t)c;
 }
 
-size_t attn_workspace(int64_t T, int64_t H, int32_t S) {
-  if (S <= 1) return 0;
+// Workspace of a split call: [partial outputs T x S x H x 512 fp32]
+// [(max, sum) T x S x H fp32].
+size_t partial_bytes(int64_t T, int64_t H, int32_t S) {
   const size_t rows = (size_t)T * (size_t)S * (size_t)H;
   return rows * dsa::kHeadDimCkv * sizeof(float) + rows * 2 * sizeof(float);
+}
+
+size_t attn_workspace(int64_t T, int64_t H, int32_t S) {
+  return S <= 1 ? 0 : partial_bytes(T, H, S);
 }
 
 }  // namespace
@@ -100,86 +105,155 @@ size_t dsa_attn_workspace_bytes(int64_t num_tokens, int64_t num_heads, int64_t t
   return attn_workspace(num_tokens, num_heads, s);
 }
 
-int dsa_attn_fwd(const dsa_attn_args *a, void *stream) {
-  if (!a) return fail(DSA_EINVAL, "dsa_attn_fwd: args is NULL");
+}  // extern "C"
+
+namespace {
+
+// Validates an attention call and fills the kernel parameters.  With
+// partial_only the fp32 partials are written (and required) for every split
+// count, and the workspace must hold them.
+int prepare_attn(const char *fn, const dsa_attn_args *a, bool partial_only, dsa::AttnParams *p) {
+  if (!a) return fail(DSA_EINVAL, "%s: args is NULL", fn);
   if (a->head_dim_ckv != dsa::kHeadDimCkv || a->head_dim_kpe != dsa::kHeadDimKpe)
-    return fail(DSA_EUNSUPPORTED, "dsa_attn_fwd: head dims must be ckv=512, kpe=64 (got %lld, %lld)",
+    return fail(DSA_EUNSUPPORTED, "%s: head dims must be ckv=512, kpe=64 (got %lld, %lld)", fn,
                 (long long)a->head_dim_ckv, (long long)a->head_dim_kpe);
   if (a->num_tokens < 0 || a->num_heads <= 0 || a->topk < 0 || a->page_size <= 0 ||
       a->num_pages < 0)
-    return fail(DSA_EINVAL, "dsa_attn_fwd: negative or zero size (T=%lld H=%lld topk=%lld "
-                "page_size=%lld num_pages=%lld)", (long long)a->num_tokens,
+    return fail(DSA_EINVAL, "%s: negative or zero size (T=%lld H=%lld topk=%lld "
+                "page_size=%lld num_pages=%lld)", fn, (long long)a->num_tokens,
                 (long long)a->num_heads, (long long)a->topk, (long long)a->page_size,
                 (long long)a->num_pages);
   if (a->num_heads % dsa::kHeadsPerGroup != 0)
-    return fail(DSA_EUNSUPPORTED, "dsa_attn_fwd: num_heads must be a multiple of 16 (got %lld)",
+    return fail(DSA_EUNSUPPORTED, "%s: num_heads must be a multiple of 16 (got %lld)", fn,
                 (long long)a->num_heads);
   if (a->num_tokens > (1 << 26) || a->topk > (1 << 30) || a->num_heads > 4096 ||
       a->page_size > (1 << 30))
-    return fail(DSA_EUNSUPPORTED, "dsa_attn_fwd: size beyond the supported range");
-  if (a->num_splits < 0) return fail(DSA_EINVAL, "dsa_attn_fwd: num_splits must be >= 0");
-  if (a->num_tokens == 0) return ok();
-  if (!a->q_nope || !a->q_pe || !a->output || !a->lse || (a->topk > 0 && !a->sparse_indices))
-    return fail(DSA_EINVAL, "dsa_attn_fwd: NULL tensor pointer");
+    return fail(DSA_EUNSUPPORTED, "%s: size beyond the supported range", fn);
+  if (a->num_splits < 0) return fail(DSA_EINVAL, "%s: num_splits must be >= 0", fn);
+  if (a->num_tokens == 0) return DSA_OK;
+  if (!a->q_nope || !a->q_pe || (!partial_only && (!a->output || !a->lse)) ||
+      (a->topk > 0 && !a->sparse_indices))
+    return fail(DSA_EINVAL, "%s: NULL tensor pointer", fn);
   if (a->num_pages > 0 && (!a->ckv || !a->kpe))
-    return fail(DSA_EINVAL, "dsa_attn_fwd: NULL cache pointer");
+    return fail(DSA_EINVAL, "%s: NULL cache pointer", fn);
   // 16-byte rows for the MFMA operand loads and the LDS DMA gathers.
   if (!aligned(a->q_nope, 16) || !aligned(a->q_pe, 16) || !aligned(a->ckv, 16) ||
       !aligned(a->kpe, 16) || (a->q_nope_stride_t * 2) % 16 || (a->q_nope_stride_h * 2) % 16 ||
       (a->q_pe_stride_t * 2) % 16 || (a->q_pe_stride_h * 2) % 16 ||
       (a->ckv_stride_page * 2) % 16 || (a->ckv_stride_tok * 2) % 16 ||
       (a->kpe_stride_page * 2) % 16 || (a->kpe_stride_tok * 2) % 16)
-    return fail(DSA_EINVAL, "dsa_attn_fwd: q/ckv/kpe rows must be 16-byte aligned");
-  if (!aligned(a->output, 8) || (a->out_stride_t * 2) % 8 || (a->out_stride_h * 2) % 8 ||
-      !aligned(a->lse, 4) || !aligned(a->sparse_indices, 4))
-    return fail(DSA_EINVAL, "dsa_attn_fwd: output rows must be 8-byte aligned");
-  const int64_t num_slots = a->num_pages * a->page_size;
+    return fail(DSA_EINVAL, "%s: q/ckv/kpe rows must be 16-byte aligned", fn);
+  if (!partial_only && (!aligned(a->output, 8) || (a->out_stride_t * 2) % 8 ||
+                        (a->out_stride_h * 2) % 8 || !aligned(a->lse, 4)))
+    return fail(DSA_EINVAL, "%s: output rows must be 8-byte aligned", fn);
+  if (!aligned(a->sparse_indices, 4))
+    return fail(DSA_EINVAL, "%s: sparse_indices must be 4-byte aligned", fn);
 
   int32_t S, chunk;
   choose_splits(a->num_tokens, a->num_heads, a->topk, a->num_splits, &S, &chunk);
   if (a->num_tokens * (int64_t)S > 0x7fffffffLL)
-    return fail(DSA_EUNSUPPORTED, "dsa_attn_fwd: num_tokens * splits exceeds the grid");
-  const size_t need = attn_workspace(a->num_tokens, a->num_heads, S);
+    return fail(DSA_EUNSUPPORTED, "%s: num_tokens * splits exceeds the grid", fn);
+  const size_t need = partial_only ? partial_bytes(a->num_tokens, a->num_heads, S)
+                                   : attn_workspace(a->num_tokens, a->num_heads, S);
   if (need > 0 && (!a->workspace || a->workspace_bytes < need || !aligned(a->workspace, 16)))
-    return fail(DSA_EWORKSPACE, "dsa_attn_fwd: workspace of %zu bytes (16-byte aligned) needed, "
-                "got %zu", need, a->workspace ? a->workspace_bytes : (size_t)0);
+    return fail(DSA_EWORKSPACE, "%s: workspace of %zu bytes (16-byte aligned) needed, got %zu",
+                fn, need, a->workspace ? a->workspace_bytes : (size_t)0);
 
-  dsa::AttnParams p;
-  p.q_nope = static_cast<const char *>(a->q_nope);
-  p.qn_st = a->q_nope_stride_t * 2;
-  p.qn_sh = a->q_nope_stride_h * 2;
-  p.q_pe = static_cast<const char *>(a->q_pe);
-  p.qp_st = a->q_pe_stride_t * 2;
-  p.qp_sh = a->q_pe_stride_h * 2;
-  p.ckv = static_cast<const char *>(a->ckv);
-  p.ckv_sp = a->ckv_stride_page * 2;
-  p.ckv_so = a->ckv_stride_tok * 2;
-  p.kpe = static_cast<const char *>(a->kpe);
-  p.kpe_sp = a->kpe_stride_page * 2;
-  p.kpe_so = a->kpe_stride_tok * 2;
-  p.idx = a->sparse_indices;
-  p.idx_st = a->idx_stride_t;
+  p->q_nope = static_cast<const char *>(a->q_nope);
+  p->qn_st = a->q_nope_stride_t * 2;
+  p->qn_sh = a->q_nope_stride_h * 2;
+  p->q_pe = static_cast<const char *>(a->q_pe);
+  p->qp_st = a->q_pe_stride_t * 2;
+  p->qp_sh = a->q_pe_stride_h * 2;
+  p->ckv = static_cast<const char *>(a->ckv);
+  p->ckv_sp = a->ckv_stride_page * 2;
+  p->ckv_so = a->ckv_stride_tok * 2;
+  p->kpe = static_cast<const char *>(a->kpe);
+  p->kpe_sp = a->kpe_stride_page * 2;
+  p->kpe_so = a->kpe_stride_tok * 2;
+  p->idx = a->sparse_indices;
+  p->idx_st = a->idx_stride_t;
+  p->out = static_cast<char *>(a->output);
+  p->out_st = a->out_stride_t * 2;
+  p->out_sh = a->out_stride_h * 2;
+  p->lse = a->lse;
+  p->lse_st = a->lse_stride_t;
+  p->lse_sh = a->lse_stride_h;
+  p->T = (int32_t)a->num_tokens;
+  p->H = (int32_t)a->num_heads;
+  p->K = (int32_t)a->topk;
+  p->page_size = (int32_t)a->page_size;
+  p->num_slots = a->num_pages * a->page_size;
+  p->scale_log2 = a->sm_scale * 1.4426950408889634f;
+  p->num_splits = S;
+  p->chunk = chunk;
+  float *ws = static_cast<float *>(a->workspace);
+  p->part_acc = ws;
+  p->part_ml = ws ? ws + (size_t)a->num_tokens * S * a->num_heads * dsa::kHeadDimCkv : nullptr;
+  p->partial_only = partial_only ? 1 : 0;
+  return DSA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dsa_attn_fwd(const dsa_attn_args *a, void *stream) {
+  dsa::AttnParams p = {};
+  const int rc = prepare_attn("dsa_attn_fwd", a, false, &p);
+  if (rc != DSA_OK) return rc;
+  if (a->num_tokens == 0) return ok();
+  const hipError_t e = dsa::launch_attention(p, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess)
+    return fail(DSA_ELAUNCH, "dsa_attn_fwd: launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int dsa_attn_fwd_partial(const dsa_attn_args *a, void *stream) {
+  dsa::AttnParams p = {};
+  const int rc = prepare_attn("dsa_attn_fwd_partial", a, true, &p);
+  if (rc != DSA_OK) return rc;
+  if (a->num_tokens == 0) return ok();
+  const hipError_t e = dsa::launch_attention_partial(p, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess)
+    return fail(DSA_ELAUNCH, "dsa_attn_fwd_partial: launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+size_t dsa_attn_partial_bytes(int64_t num_tokens, int64_t num_heads, int64_t topk,
+                              int32_t requested_splits) {
+  int32_t s, c;
+  choose_splits(num_tokens, num_heads, topk, requested_splits, &s, &c);
+  return partial_bytes(num_tokens, num_heads, s);
+}
+
+int dsa_attn_merge(const dsa_attn_merge_args *a, void *stream) {
+  if (!a) return fail(DSA_EINVAL, "dsa_attn_merge: args is NULL");
+  if (a->num_tokens < 0 || a->num_splits <= 0 || a->num_heads <= 0 ||
+      a->num_tokens * a->num_splits > 0x7fffffffLL || a->num_heads > 65535)
+    return fail(DSA_EINVAL, "dsa_attn_merge: bad sizes (T=%lld S=%lld H=%lld)",
+                (long long)a->num_tokens, (long long)a->num_splits, (long long)a->num_heads);
+  if (a->num_tokens == 0) return ok();
+  if (!a->part_acc || !a->part_ml || !a->output || !a->lse)
+    return fail(DSA_EINVAL, "dsa_attn_merge: NULL pointer");
+  if (!aligned(a->part_acc, 16) || !aligned(a->part_ml, 8) || !aligned(a->output, 8) ||
+      (a->out_stride_t * 2) % 8 || (a->out_stride_h * 2) % 8 || !aligned(a->lse, 4))
+    return fail(DSA_EINVAL, "dsa_attn_merge: misaligned pointer or stride");
+  dsa::AttnParams p = {};
+  p.T = (int32_t)a->num_tokens;
+  p.H = (int32_t)a->num_heads;
+  p.num_splits = (int32_t)a->num_splits;
+  p.part_acc = const_cast<float *>(a->part_acc);
+  p.part_ml = const_cast<float *>(a->part_ml);
   p.out = static_cast<char *>(a->output);
   p.out_st = a->out_stride_t * 2;
   p.out_sh = a->out_stride_h * 2;
   p.lse = a->lse;
   p.lse_st = a->lse_stride_t;
   p.lse_sh = a->lse_stride_h;
-  p.T = (int32_t)a->num_tokens;
-  p.H = (int32_t)a->num_heads;
-  p.K = (int32_t)a->topk;
-  p.page_size = (int32_t)a->page_size;
-  p.num_slots = num_slots;
-  p.scale_log2 = a->sm_scale * 1.4426950408889634f;
-  p.num_splits = S;
-  p.chunk = chunk;
-  float *ws = static_cast<float *>(a->workspace);
-  p.part_acc = ws;
-  p.part_ml = ws ? ws + (size_t)a->num_tokens * S * a->num_heads * dsa::kHeadDimCkv : nullptr;
-
-  const hipError_t e = dsa::launch_attention(p, static_cast<hipStream_t>(stream));
+  const hipError_t e = dsa::launch_attention_merge(p, static_cast<hipStream_t>(stream));
   if (e != hipSuccess)
-    return fail(DSA_ELAUNCH, "dsa_attn_fwd: launch failed: %s", hipGetErrorString(e));
+    return fail(DSA_ELAUNCH, "dsa_attn_merge: launch failed: %s", hipGetErrorString(e));
   return ok();
 }
 

@@ -14,10 +14,11 @@
 // head groups).  Its waves share a 3-stage LDS ring of 32-key tiles: every
 // tile is gathered with global_load_lds_dwordx4 (16 B per lane straight into
 // LDS, no VGPR staging; one 1 KB ckv row per instruction, 8 kpe rows per
-// instruction), two tiles in flight while the third is consumed.  The chunk's
-// slot ids are staged in LDS once, so issuing a tile's gathers never waits on
-// an index load.  Padding keys gather a zero row, which keeps the number of
-// loads per wave and tile fixed and makes the vmcnt-based stage waits exact.
+// instruction), two tiles in flight while the third is consumed.  The gather
+// addresses of the chunk's keys and a valid-key mask per tile are staged in
+// LDS once, so issuing a tile's gathers never waits on an index load or a
+// division.  Padding keys gather a zero row, which keeps the number of loads
+// per wave and tile fixed and makes the vmcnt-based stage waits exact.
 //
 // Each wave belongs to one 16-head group and owns one slice of the 512 output
 // features.  Per tile:
@@ -25,15 +26,22 @@
 //     -- when FS > 1 waves share a head group, they split the 2 key blocks x
 //        18 k-steps of this product and add the partial S^T through LDS in a
 //        fixed order, so every wave of the group holds identical scores;
-//   online softmax in fp32 (log2 domain);
+//   online softmax in fp32 (log2 domain), with the reference max moved only
+//   when scores overshoot it by more than kRescaleSlack;
 //   O^T[slice x 16 heads] += V^T[slice x 32 keys] . P^T  (bf16 MFMA 16x16x32,
 //     P split into bf16 hi + lo parts, ~16-bit P; the V^T operand is read
 //     with ds_read_b64_tr_b16, which transposes 16-bit elements across lanes).
 // Computing S^T (keys as the MFMA M dimension) leaves P^T in exactly the lane
-// layout the PV product takes as its B operand.  A workgroup writes either the
-// final bf16 output and lse (one chunk per token) or an unnormalised fp32
-// partial that dsa_attn_combine_kernel merges with log-sum-exp weights
-// (reference merge algebra: kernel.py:461-493).
+// layout the PV product takes as its B operand.
+//
+// Splits.  With one chunk per token the workgroup writes the bf16 output and
+// lse directly.  Otherwise each workgroup writes an unnormalised fp32 partial
+// (acc, m, l) and dsa_attn_combine_kernel merges a token's partials with
+// log-sum-exp weights in split order (reference merge algebra:
+// kernel.py:461-493, -inf guards :475-476), so results are deterministic.
+// (Merging inside the gather kernel, last-arriving workgroup style, needs a
+// device-scope release per workgroup -- an L2 write-back on this part -- and
+// measured slower than the second launch.)
 //
 // MFMA 16x16x32 bf16 lane layout used throughout (lane = 16*g + r):
 //   A (16 x 32): lane holds row r, k-slots 8g..8g+7
@@ -41,6 +49,13 @@
 //   D (16 x 16): lane holds column r, rows 4g..4g+3
 // Only the A/B k-slot assignment being identical matters for a product, so
 // the kernel assigns k-slots to features or keys as convenient.
+//
+// Within a 16-key block, MFMA row m of S^T holds key pi(m) = 8*((m>>2)&1) +
+// (m>>3) + 2*(m&3), so lane group g owns keys kbase(g) + {0,2,4,6} with
+// kbase = 0, 8, 1, 9.  The QK operand reads still touch 16 distinct rows
+// (conflict-free with the 1040-byte pitch), and the PV transpose reads of one
+// 32-lane half touch 8 rows whose 32-byte pieces land on 8 disjoint bank
+// ranges, which is conflict-free too.
 //
 // ds_read_b64_tr_b16, per 16-lane group: lane i receives element i%4 of the
 // 4-element (8-byte) rows addressed by lanes 4j + i/4, j = 0..3.  Pointing
@@ -67,10 +82,16 @@ constexpr int kKpeGroupPitch = 1024 + 128;
 constexpr int kCkvStageBytes = kKeysPerTile * kCkvPitch;
 constexpr int kStageBytes = kCkvStageBytes + (kKeysPerTile / 8) * kKpeGroupPitch;
 constexpr int kStages = 3;
-constexpr int kIdxBytes = kMaxChunk * 4;
-constexpr int kXchgBytes = 8 * 64 * 16;  // one f32x4 per lane per wave
-constexpr int kLdsBytes = kStages * kStageBytes + kIdxBytes + kXchgBytes;
+constexpr int kAddrBytes = kMaxChunk * 8;                   // one row address per key
+constexpr int kMaskBytes = kMaxChunk / kKeysPerTile * 4;    // valid-key bits per tile
+constexpr int kXchgBytes = 8 * 64 * 16;                     // one f32x4 per lane per wave
+constexpr int kLdsBytes = kStages * kStageBytes + 2 * kAddrBytes + kMaskBytes + kXchgBytes;
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one gfx950 CU");
+
+// The running max is only moved (and the accumulator rescaled) when a head's
+// scores exceed it by more than this many log2 units, so probabilities stay
+// below 2^8 and most tiles skip the rescale entirely.
+constexpr float kRescaleSlack = 8.0f;
 
 // Padding keys gather from here (global memory, never written).
 __device__ __attribute__((aligned(64))) const uint4 g_zero_row[64] = {};
@@ -94,6 +115,11 @@ __device__ __forceinline__ uint64_t readlane64(uint64_t v, int lane) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Key (within a 16-key block) that MFMA row m of S^T stands for.
+__device__ __forceinline__ int key_of_row(int m) {
+  return ((m >> 2) & 1) * 8 + (m >> 3) + 2 * (m & 3);
+}
+
 // Waits until at most N of this wave's vector-memory operations are
 // outstanding (they complete in issue order).
 template <int N>
@@ -102,49 +128,92 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Partial S^T over k-steps S0..S0+N-1 (step s < 16: ckv features 32s..;
+// s = 16, 17: kpe) for this lane's key row rowp / kpe chunk base kp.
+template <int S0, int N>
+__device__ __forceinline__ f32x4 qk_steps(const char *rowp, const char *kp, const bf16x8 *q,
+                                          int g) {
+  f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    const int s = S0 + k;
+    const char *ap = s < 16 ? rowp + s * 64 : kp + ((s - 16) * 4 + g) * 128;
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)ap, q[k], c, 0, 0, 0);
+  }
+  return c;
+}
+
+// k-step range [first(P), first(P+1)) of part P when 18 steps are cut into NP.
+template <int NP>
+struct Parts {
+  static constexpr int first(int part) { return part * 18 / NP; }
+  static constexpr int count(int part) { return first(part + 1) - first(part); }
+  static constexpr int kMax = (18 + NP - 1) / NP;
+};
+
+template <int NP>
+__device__ __forceinline__ f32x4 qk_part(int part, const char *rowp, const char *kp,
+                                         const bf16x8 *q, int g) {
+  using P = Parts<NP>;
+  if (NP == 1) return qk_steps<0, 18>(rowp, kp, q, g);
+  if (NP == 2) {
+    if (part == 0) return qk_steps<0, P::count(0)>(rowp, kp, q, g);
+    return qk_steps<P::first(1), P::count(1)>(rowp, kp, q, g);
+  }
+  switch (part) {
+    case 0: return qk_steps<0, P::count(0)>(rowp, kp, q, g);
+    case 1: return qk_steps<P::first(1), P::count(1)>(rowp, kp, q, g);
+    case 2: return qk_steps<P::first(2), P::count(2)>(rowp, kp, q, g);
+    default: return qk_steps<P::first(3), P::count(3)>(rowp, kp, q, g);
+  }
+}
+
 // W waves per workgroup; FS waves share one 16-head group, each owning
 // 512/FS output features.  W/FS head groups per workgroup.  With FS > 1 the
-// waves of a group split S^T = K Q^T: 2 key blocks x kParts step ranges.
+// waves of a group split S^T = K Q^T into 2 key blocks x kParts step ranges.
 template <int W, int FS>
 struct Ring {
   static constexpr int kHG = W / FS;
   static constexpr int kNFB = 32 / FS;            // 16-feature blocks per wave
   static constexpr int kRows = kKeysPerTile / W;  // ckv rows one wave gathers per tile
   static constexpr int kLoads = kRows + 1;        // + one kpe DMA (full or half)
-  static constexpr int kParts = FS >= 2 ? FS / 2 : 1;              // k-step ranges per block
-  static constexpr int kBlocks = FS >= 2 ? 1 : 2;                  // key blocks one wave computes
-  static constexpr int kSteps = 18 / kParts;                       // k-steps per range
+  static constexpr int kParts = FS >= 2 ? FS / 2 : 1;  // k-step ranges per key block
+  static constexpr int kBlocks = FS >= 2 ? 1 : 2;      // key blocks one wave computes
+  static constexpr int kQRegs = Parts<kParts>::kMax;   // Q operand registers (x4 VGPRs)
   static_assert(W == 4 || W == 8, "gather split assumes 4 or 8 waves");
-  static_assert(FS == 1 || FS == 2 || FS == 4, "feature slices");
-  static_assert(18 % kParts == 0, "k-step split");
+  static_assert(FS == 1 || FS == 2 || FS == 4 || FS == 8, "feature slices");
 };
 
 template <int W, int FS>
 __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) {
   using R = Ring<W, FS>;
   __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
-  int32_t *lds_idx = (int32_t *)(lds + kStages * kStageBytes);
-  f32x4 *xbuf = (f32x4 *)(lds + kStages * kStageBytes + kIdxBytes);
+  uint64_t *ckv_rows = (uint64_t *)(lds + kStages * kStageBytes);
+  uint64_t *kpe_rows = ckv_rows + kMaxChunk;
+  uint32_t *tile_mask = (uint32_t *)(kpe_rows + kMaxChunk);
+  f32x4 *xbuf = (f32x4 *)(lds + kStages * kStageBytes + 2 * kAddrBytes + kMaskBytes);
+
+  const int t = blockIdx.x / p.num_splits;
+  const int split = blockIdx.x - t * p.num_splits;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int t = blockIdx.x / p.num_splits;
-  const int split = blockIdx.x - t * p.num_splits;
   const int r16 = lane & 15;
   const int g = lane >> 4;
   const int hg = wave / FS;
   const int fs = wave - hg * FS;
   const int head = (blockIdx.y * R::kHG + hg) * kHeadsPerGroup + r16;
-  // this wave's share of S^T: key block qb0 (+1 if kBlocks == 2), steps s0..
+  // this wave's share of S^T: key block qb0 (+1 if kBlocks == 2), step range part
   const int qb0 = FS >= 2 ? (fs & 1) : 0;
-  const int s0 = FS >= 2 ? (fs >> 1) * R::kSteps : 0;
+  const int part = FS >= 2 ? (fs >> 1) : 0;
 
   const int k_begin = split * p.chunk;
   const int n_keys = max(0, min(p.K, k_begin + p.chunk) - k_begin);
   const int n_tiles = (n_keys + kKeysPerTile - 1) / kKeysPerTile;
 
-  // ---- stage the chunk's slot ids (invalid -> -1), padded to whole tiles;
-  // all loads are issued before the first store so they overlap
+  // ---- stage the gather addresses of the chunk's keys (padding and invalid
+  // ids -> the zero row) and one valid-key mask per tile; all index loads are
+  // issued before the first store so they overlap
   {
     constexpr int kPer = kMaxChunk / (W * 64);
     const int32_t *src = p.idx + (int64_t)t * p.idx_st + k_begin;
@@ -154,53 +223,62 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
       const int i = threadIdx.x + k * W * 64;
       sv[k] = i < n_keys ? src[i] : -1;
     }
+    const uint64_t zero_row = (uint64_t)(const char *)g_zero_row;
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
       const int i = threadIdx.x + k * W * 64;
       const int s = sv[k];
-      if (i < n_tiles * kKeysPerTile) lds_idx[i] = (s < 0 || (int64_t)s >= p.num_slots) ? -1 : s;
+      const bool valid = s >= 0 && (int64_t)s < p.num_slots;
+      uint64_t ca = zero_row, ka = zero_row;
+      if (valid) {
+        const uint32_t pg = (uint32_t)s / (uint32_t)p.page_size;
+        const uint32_t of = (uint32_t)s - pg * (uint32_t)p.page_size;
+        ca = (uint64_t)(p.ckv + (int64_t)pg * p.ckv_sp + (int64_t)of * p.ckv_so);
+        ka = (uint64_t)(p.kpe + (int64_t)pg * p.kpe_sp + (int64_t)of * p.kpe_so);
+      }
+      const uint64_t bits = __ballot(valid);  // lanes 0-31: tile i/32, 32-63: the next
+      if (i < n_tiles * kKeysPerTile) {
+        ckv_rows[i] = ca;
+        kpe_rows[i] = ka;
+        if ((lane & 31) == 0) tile_mask[i / kKeysPerTile] = (uint32_t)(bits >> (lane & 32));
+      }
     }
   }
 
   // Q^T as the B operand of S^T = K Q^T: k-step s covers features 32s..32s+31
   // (s < 16: q_nope; s = 16, 17: q_pe); this lane holds 8g..8g+7 of them.
-  bf16x8 qreg[R::kSteps];
+  bf16x8 qreg[R::kQRegs];
   {
+    const int s0 = Parts<R::kParts>::first(part);
+    const int ns = Parts<R::kParts>::first(part + 1) - s0;
     const char *qn = p.q_nope + t * p.qn_st + head * p.qn_sh + g * 16;
     const char *qp = p.q_pe + t * p.qp_st + head * p.qp_sh + g * 16;
 #pragma unroll
-    for (int k = 0; k < R::kSteps; ++k) {
+    for (int k = 0; k < R::kQRegs; ++k) {
       const int s = s0 + k;
-      qreg[k] = *(const bf16x8 *)(s < 16 ? qn + s * 64 : qp + (s - 16) * 64);
+      if (k < ns) qreg[k] = *(const bf16x8 *)(s < 16 ? qn + s * 64 : qp + (s - 16) * 64);
     }
   }
   // Retire the Q loads with a wait the compiler sees (s_waitcnt vmcnt(0)), so
   // its own bookkeeping has nothing outstanding when the gather ring starts
   // and it adds no drain at the loop header.
   __builtin_amdgcn_s_waitcnt(0x0F70);
-  __syncthreads();  // slot ids visible; nothing gathered yet
+  __syncthreads();  // addresses and masks visible; nothing gathered yet
 
   // ---- gather issue: this wave's share of tile j into stage j % kStages.
-  // Lane l owns the slot of key 8*grp + (l & 7) of the tile, grp being the
-  // kpe group (8 rows) this wave gathers (a half group when W == 8).
+  // Lane l owns key 8*grp + (l & 7) of the tile, grp being the kpe group
+  // (8 rows) this wave gathers (a half group when W == 8).
   const int grp = (W == 4) ? wave : (wave >> 1);
   const int row0 = (W == 4) ? 0 : 4 * (wave & 1);  // first ckv row within the group
   auto issue_tile = [&](int j) {
     char *st = lds + (j % kStages) * kStageBytes;
-    const int s = lds_idx[j * kKeysPerTile + grp * 8 + (lane & 7)];
-    uint64_t ckv_addr = (uint64_t)(const char *)g_zero_row;
-    uint64_t kpe_addr = ckv_addr;
-    if (s >= 0) {
-      const uint32_t pg = (uint32_t)s / (uint32_t)p.page_size;
-      const uint32_t of = (uint32_t)s - pg * (uint32_t)p.page_size;
-      ckv_addr = (uint64_t)(p.ckv + (int64_t)pg * p.ckv_sp + (int64_t)of * p.ckv_so);
-      kpe_addr = (uint64_t)(p.kpe + (int64_t)pg * p.kpe_sp + (int64_t)of * p.kpe_so);
-    }
+    const int key = j * kKeysPerTile + grp * 8 + (lane & 7);
+    const uint64_t ckv_addr = ckv_rows[key];
+    const uint64_t kpe_addr = kpe_rows[key];
 #pragma unroll
     for (int m = 0; m < R::kRows; ++m) {
-      const int key = grp * 8 + row0 + m;
       const char *src = (const char *)readlane64(ckv_addr, row0 + m) + lane * 16;
-      lds_dma16(src, st + key * kCkvPitch);
+      lds_dma16(src, st + (grp * 8 + row0 + m) * kCkvPitch);
     }
     char *kdst = st + kCkvStageBytes + grp * kKpeGroupPitch;
     const char *ksrc = (const char *)kpe_addr + (lane >> 3) * 16;
@@ -210,7 +288,7 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
   f32x4 acc[R::kNFB];
 #pragma unroll
   for (int i = 0; i < R::kNFB; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY;  // running max of x*log2(e) for this lane's head
+  float m_run = -INFINITY;  // reference max of x*log2(e) for this lane's head
   float l_run = 0.f;        // running sum over this lane's keys (reduced at the end)
 
   const int pre = min(n_tiles, kStages - 1);
@@ -226,24 +304,17 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
 
     const char *st_ckv = lds + (i % kStages) * kStageBytes;
     const char *st_kpe = st_ckv + kCkvStageBytes;
-    const uint32_t vmask = (uint32_t)__ballot(lds_idx[i * kKeysPerTile + (lane & 31)] >= 0);
+    const uint32_t vmask = tile_mask[i];
 
     // ---- S^T = K . Q^T (this wave's blocks and k-steps)
     f32x4 sacc[2];
 #pragma unroll
     for (int bb = 0; bb < R::kBlocks; ++bb) {
       const int b = qb0 + bb;
-      f32x4 c = {0.f, 0.f, 0.f, 0.f};
-      const char *rowp = st_ckv + (b * 16 + r16) * kCkvPitch + g * 16;
-      const int kk = b * 16 + r16;
+      const int kk = b * 16 + key_of_row(r16);
+      const char *rowp = st_ckv + kk * kCkvPitch + g * 16;
       const char *kp = st_kpe + (kk >> 3) * kKpeGroupPitch + (kk & 7) * 16;
-#pragma unroll
-      for (int k = 0; k < R::kSteps; ++k) {
-        const int s = s0 + k;
-        const char *ap = s < 16 ? rowp + s * 64 : kp + ((s - 16) * 4 + g) * 128;
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)ap, qreg[k], c, 0, 0, 0);
-      }
-      sacc[bb] = c;
+      sacc[bb] = qk_part<R::kParts>(part, rowp, kp, qreg, g);
     }
     if (FS >= 2) {
       // partial scores of the group's waves, added in a fixed order
@@ -255,54 +326,80 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
       for (int b = 0; b < 2; ++b) {
         f32x4 c = xbuf[(base + b) * 64 + lane];
 #pragma unroll
-        for (int part = 1; part < R::kParts; ++part) c += xbuf[(base + b + 2 * part) * 64 + lane];
+        for (int pp = 1; pp < R::kParts; ++pp) c += xbuf[(base + b + 2 * pp) * 64 + lane];
         sacc[b] = c;
       }
     }
 
-    // ---- online softmax (this lane: head r16, keys b*16 + 4g + k)
-    float x[8];
-    float mx = -INFINITY;
+    // ---- online softmax.  This lane: head r16; slot (b, k) holds key
+    // b*16 + kbase + 2k.  d = x*log2(e) - m_run with the lazily moved
+    // reference m_run; the tile max is only reduced when some score
+    // overshoots the reference by more than the slack (always on the first
+    // valid tile, where m_run = -inf).
+    const int kbase = (g & 1) * 8 + (g >> 1);
+    const uint32_t vm = vmask >> kbase;
+    const bool full = vmask == 0xffffffffu;  // wave-uniform
+    const float c = p.scale_log2;
+    float d[8];
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const int key = b * 16 + 4 * g + k;
-        const float v = ((vmask >> key) & 1u) ? sacc[b][k] * p.scale_log2 : -INFINITY;
-        x[b * 4 + k] = v;
-        mx = fmaxf(mx, v);
+        const float v = __builtin_fmaf(sacc[b][k], c, -m_run);
+        d[b * 4 + k] = (full || ((vm >> (b * 16 + 2 * k)) & 1u)) ? v : -INFINITY;
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const bool none = m_new == -INFINITY;
-    const float alpha = none ? 1.f : fast_exp2(m_run - m_new);
+    bool over = false;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) over |= d[k] > kRescaleSlack;
+    if (__ballot(over) != 0) {  // wave-uniform
+      float mx = -INFINITY;
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (full || ((vm >> (b * 16 + 2 * k)) & 1u)) mx = fmaxf(mx, sacc[b][k] * c);
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int fb = 0; fb < R::kNFB; ++fb) acc[fb] *= alpha;
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float v = __builtin_fmaf(sacc[b][k], c, -m_run);
+          d[b * 4 + k] = (full || ((vm >> (b * 16 + 2 * k)) & 1u)) ? v : -INFINITY;
+        }
+    }
+    // m_run stays -inf only while no valid key has been seen; then every
+    // d is -inf and the probabilities are 0.
     bf16x8 p_hi, p_lo;
     float psum = 0.f;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const float pv = none ? 0.f : fast_exp2(x[k] - m_new);
+      const float pv = fast_exp2(d[k]);
       psum += pv;
       p_hi[k] = (__bf16)pv;
       p_lo[k] = (__bf16)(pv - (float)p_hi[k]);
     }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
+    l_run += psum;
 
     // ---- O^T += V^T . P^T over this wave's feature slice; k-slot k of lane
-    // group g is key 4g+k (k < 4) or 16+4g+(k-4).
+    // group g is key kbase+2k (k < 4) or 16+kbase+2(k-4).
     if (FS >= 2) {
-      // Lane 16g+s points the transpose read at key row 4g + s/4 (+16),
-      // features f0 + 4*(s%4).
-      const char *vsrc = st_ckv + (4 * g + (r16 >> 2)) * kCkvPitch +
+      // Lane 16g+s points the transpose read at key row kbase + 2*(s/4)
+      // (+16 for slots 4..7), features f0 + 4*(s%4).
+      const char *vsrc = st_ckv + (kbase + 2 * (r16 >> 2)) * kCkvPitch +
                          (fs * R::kNFB * 16 + 4 * (r16 & 3)) * 2;
 #pragma unroll
       for (int fb = 0; fb < R::kNFB; ++fb) {
         const bf16x4 lo4 = lds_read_tr16(vsrc + fb * 32);
         const bf16x4 hi4 = lds_read_tr16(vsrc + 16 * kCkvPitch + fb * 32);
         const bf16x8 av = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
-        f32x4 c = acc[fb] * alpha;
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, p_hi, c, 0, 0, 0);
+        const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, p_hi, acc[fb], 0, 0, 0);
         acc[fb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, p_lo, c, 0, 0, 0);
       }
     } else {
@@ -313,15 +410,14 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
       const char *vrow[8];
 #pragma unroll
       for (int k = 0; k < 8; ++k)
-        vrow[k] = vcol + ((k < 4) ? (4 * g + k) : (16 + 4 * g + k - 4)) * kCkvPitch;
+        vrow[k] = vcol + ((k < 4) ? (kbase + 2 * k) : (16 + kbase + 2 * (k - 4))) * kCkvPitch;
 #pragma unroll
       for (int fb = 0; fb < R::kNFB; ++fb) {
         u16x8 a;
 #pragma unroll
         for (int k = 0; k < 8; ++k) a[k] = *(const unsigned short *)(vrow[k] + fb * 32);
         const bf16x8 av = __builtin_bit_cast(bf16x8, a);
-        f32x4 c = acc[fb] * alpha;
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, p_hi, c, 0, 0, 0);
+        const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, p_hi, acc[fb], 0, 0, 0);
         acc[fb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, p_lo, c, 0, 0, 0);
       }
     }
@@ -330,29 +426,32 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
   // ---- epilogue: lanes of a head hold partial sums over disjoint keys
   l_run += __shfl_xor(l_run, 16);
   l_run += __shfl_xor(l_run, 32);
-  const bool final_out = p.num_splits == 1;
-  const float inv = (m_run == -INFINITY) ? 0.f : 1.f / l_run;
-  const int64_t prow = ((int64_t)t * p.num_splits + split) * p.H + head;
+  if (p.num_splits == 1 && !p.partial_only) {
+    const float inv = (m_run == -INFINITY) ? 0.f : 1.f / l_run;
 #pragma unroll
-  for (int fb = 0; fb < R::kNFB; ++fb) {
-    const int f0 = (fs * R::kNFB + fb) * 16 + 4 * g;
-    if (final_out) {
+    for (int fb = 0; fb < R::kNFB; ++fb) {
+      const int f0 = (fs * R::kNFB + fb) * 16 + 4 * g;
       bf16x4 ob;
 #pragma unroll
       for (int k = 0; k < 4; ++k) ob[k] = (__bf16)(acc[fb][k] * inv);
       *(bf16x4 *)(p.out + t * p.out_st + head * p.out_sh + f0 * 2) = ob;
-    } else {
-      *(f32x4 *)(p.part_acc + prow * kHeadDimCkv + f0) = acc[fb];
     }
-  }
-  if (fs == 0 && lane < 16) {
-    if (final_out) {
+    if (fs == 0 && lane < 16)
       p.lse[t * p.lse_st + head * p.lse_sh] =
           (m_run == -INFINITY) ? -INFINITY : m_run + __log2f(l_run);
-    } else {
-      p.part_ml[prow * 2 + 0] = m_run;
-      p.part_ml[prow * 2 + 1] = l_run;
-    }
+    return;
+  }
+
+  // ---- split: write this chunk's partial for dsa_attn_combine_kernel
+  const int64_t prow = ((int64_t)t * p.num_splits + split) * p.H + head;
+#pragma unroll
+  for (int fb = 0; fb < R::kNFB; ++fb) {
+    const int f0 = (fs * R::kNFB + fb) * 16 + 4 * g;
+    *(f32x4 *)(p.part_acc + prow * kHeadDimCkv + f0) = acc[fb];
+  }
+  if (fs == 0 && lane < 16) {
+    p.part_ml[prow * 2 + 0] = m_run;
+    p.part_ml[prow * 2 + 1] = l_run;
   }
 }
 
@@ -386,29 +485,43 @@ __global__ __launch_bounds__(128) void dsa_attn_combine_kernel(AttnParams p) {
     p.lse[t * p.lse_st + head * p.lse_sh] = (M == -INFINITY) ? -INFINITY : M + __log2f(L);
 }
 
+template <int W, int FS>
+hipError_t launch_ring(const AttnParams &p, int head_blocks, hipStream_t stream) {
+  hipLaunchKernelGGL((dsa_attn_ring_kernel<W, FS>), dim3(p.T * p.num_splits, head_blocks),
+                     dim3(W * 64), 0, stream, p);
+  return hipGetLastError();
+}
+
 }  // namespace
 
-hipError_t launch_attention(const AttnParams &p, hipStream_t stream) {
+int attn_head_blocks(int H) {
+  const int groups = H / kHeadsPerGroup;
+  if (groups % 8 == 0) return groups / 8;
+  if (groups % 4 == 0) return groups / 4;
+  if (groups % 2 == 0) return groups / 2;
+  return groups;
+}
+
+hipError_t launch_attention_partial(const AttnParams &p, hipStream_t stream) {
   if (p.T == 0) return hipSuccess;
   const int groups = p.H / kHeadsPerGroup;
-  if (groups % 8 == 0) {
-    // 8 waves, one per 16-head group, all 512 features each
-    hipLaunchKernelGGL((dsa_attn_ring_kernel<8, 1>), dim3(p.T * p.num_splits, groups / 8),
-                       dim3(8 * 64), 0, stream, p);
-  } else if (groups % 4 == 0) {
-    hipLaunchKernelGGL((dsa_attn_ring_kernel<4, 1>), dim3(p.T * p.num_splits, groups / 4),
-                       dim3(4 * 64), 0, stream, p);
-  } else if (groups % 2 == 0) {
-    hipLaunchKernelGGL((dsa_attn_ring_kernel<4, 2>), dim3(p.T * p.num_splits, groups / 2),
-                       dim3(4 * 64), 0, stream, p);
-  } else {
-    hipLaunchKernelGGL((dsa_attn_ring_kernel<4, 4>), dim3(p.T * p.num_splits, groups),
-                       dim3(4 * 64), 0, stream, p);
-  }
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess || p.num_splits == 1) return e;
+  const int hb = attn_head_blocks(p.H);
+  if (groups % 8 == 0) return launch_ring<8, 1>(p, hb, stream);  // one wave per head group
+  if (groups % 4 == 0) return launch_ring<4, 1>(p, hb, stream);
+  if (groups % 2 == 0) return launch_ring<8, 4>(p, hb, stream);  // 2 groups x 4 slices
+  return launch_ring<8, 8>(p, hb, stream);                       // 1 group x 8 slices
+}
+
+hipError_t launch_attention_merge(const AttnParams &p, hipStream_t stream) {
+  if (p.T == 0) return hipSuccess;
   hipLaunchKernelGGL(dsa_attn_combine_kernel, dim3(p.T, p.H), dim3(128), 0, stream, p);
   return hipGetLastError();
+}
+
+hipError_t launch_attention(const AttnParams &p, hipStream_t stream) {
+  hipError_t e = launch_attention_partial(p, stream);
+  if (e != hipSuccess || (p.num_splits == 1 && !p.partial_only)) return e;
+  return launch_attention_merge(p, stream);
 }
 
 }  // namespace dsa

@@ -39,10 +39,19 @@ struct AttnParams {
   float scale_log2;  // sm_scale * log2(e)
   int32_t num_splits, chunk;
   float *part_acc;  // [T][S][H][512] unnormalised partial outputs
-  float *part_ml;   // [T][S][H][2]   (running max in log2 units, sum)
+  float *part_ml;   // [T][S][H][2]   (reference max in log2 units, sum)
+  int32_t partial_only;  // write partials even when num_splits == 1
 };
 
+// Workgroups per token along the head axis (each covers up to 8 groups of 16).
+int attn_head_blocks(int H);
+
+// Whole call: per-chunk attention, then (num_splits > 1) the merge.
 hipError_t launch_attention(const AttnParams &p, hipStream_t stream);
+// The two halves on their own: with num_splits > 1 the first writes only the
+// partials; the second merges part_acc/part_ml into out/lse.
+hipError_t launch_attention_partial(const AttnParams &p, hipStream_t stream);
+hipError_t launch_attention_merge(const AttnParams &p, hipStream_t stream);
 
 struct IndexerParams {
   const uint8_t *q;       // [T][Hi][128] e4m3 codes

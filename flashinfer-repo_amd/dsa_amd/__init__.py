@@ -9,6 +9,8 @@ Hand-written HIP kernels behind a C ABI (``include/dsa_abi.h``,
   (reference ``solution/triton/indexer_kernel.py``)
 * ``dsa_amd.workloads``: seeded synthetic inputs for the benchmark configs
 """
-from .kernel import kernel, kernel_out, kernel_splitk, kernel_splitk_v2, num_splits  # noqa: F401
+from .kernel import (kernel, kernel_out, kernel_partial, kernel_splitk, kernel_splitk_v2,  # noqa: F401
+                     merge_partials, new_workspace, num_splits)
 
-__all__ = ["kernel", "kernel_splitk", "kernel_splitk_v2", "kernel_out", "num_splits"]
+__all__ = ["kernel", "kernel_splitk", "kernel_splitk_v2", "kernel_out", "kernel_partial",
+           "merge_partials", "new_workspace", "num_splits"]

@@ -20,7 +20,10 @@ ABI_VERSION = 1
 
 EXPORTED_SYMBOLS = (
     "dsa_attn_fwd",
+    "dsa_attn_fwd_partial",
+    "dsa_attn_merge",
     "dsa_attn_num_splits",
+    "dsa_attn_partial_bytes",
     "dsa_attn_workspace_bytes",
     "dsa_indexer_topk",
     "dsa_indexer_workspace_bytes",
@@ -49,6 +52,17 @@ class AttnArgs(ctypes.Structure):
         ("sm_scale", ctypes.c_float),
         ("num_splits", ctypes.c_int32),
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+class MergeArgs(ctypes.Structure):
+    """Mirror of ``dsa_attn_merge_args``."""
+
+    _fields_ = [
+        ("part_acc", _vp), ("part_ml", _vp),
+        ("num_tokens", _i64), ("num_splits", _i64), ("num_heads", _i64),
+        ("output", _vp), ("out_stride_t", _i64), ("out_stride_h", _i64),
+        ("lse", _vp), ("lse_stride_t", _i64), ("lse_stride_h", _i64),
     ]
 
 
@@ -93,6 +107,12 @@ def load() -> ctypes.CDLL:
             raise RuntimeError(f"{LIB_PATH} does not export {name}")
     lib.dsa_attn_fwd.argtypes = [ctypes.POINTER(AttnArgs), _vp]
     lib.dsa_attn_fwd.restype = ctypes.c_int
+    lib.dsa_attn_fwd_partial.argtypes = [ctypes.POINTER(AttnArgs), _vp]
+    lib.dsa_attn_fwd_partial.restype = ctypes.c_int
+    lib.dsa_attn_merge.argtypes = [ctypes.POINTER(MergeArgs), _vp]
+    lib.dsa_attn_merge.restype = ctypes.c_int
+    lib.dsa_attn_partial_bytes.argtypes = [_i64, _i64, _i64, ctypes.c_int32]
+    lib.dsa_attn_partial_bytes.restype = ctypes.c_size_t
     lib.dsa_attn_num_splits.argtypes = [_i64, _i64, _i64, ctypes.c_int32]
     lib.dsa_attn_num_splits.restype = ctypes.c_int32
     lib.dsa_attn_workspace_bytes.argtypes = [_i64, _i64, _i64, ctypes.c_int32]

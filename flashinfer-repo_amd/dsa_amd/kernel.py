@@ -35,6 +35,15 @@ def _stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+def new_workspace(q_nope: torch.Tensor, topk: int, num_splits: int = 0) -> torch.Tensor:
+    """A workspace for calls of this shape, for callers that manage their own
+    (e.g. to keep allocation out of a serving loop); pass it to
+    :func:`kernel_out`.  Its contents do not matter."""
+    T, H, _ = q_nope.shape
+    nbytes = _lib.load().dsa_attn_workspace_bytes(T, H, topk, int(num_splits))
+    return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q_nope.device)
+
+
 def _inner_contiguous(x: torch.Tensor) -> torch.Tensor:
     return x if x.stride(-1) == 1 else x.contiguous()
 
@@ -57,8 +66,10 @@ def _cache_view(cache: torch.Tensor, dim: int, name: str) -> Tuple[torch.Tensor,
     raise ValueError(f"{name} must be [pages, page_size, {dim}] or [slots, {dim}]")
 
 
-def _attention(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, num_splits: int,
-               output: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None):
+def _attn_args(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, num_splits: int):
+    """Validate the reference tensor contract (``kernel.py:138-151``) and build
+    the ``dsa_attn_args`` struct; returns ``(args, keep_alive, T, H, K, dev)``
+    with output/lse/workspace still unset."""
     _check(q_nope.dim() == 3 and q_pe.dim() == 3, "q_nope/q_pe must be [T, H, D]")
     T, H, dc = q_nope.shape
     _check(dc == HEAD_DIM_CKV, f"q_nope head dim must be {HEAD_DIM_CKV}, got {dc}")
@@ -70,6 +81,7 @@ def _attention(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, num
     _check(sparse_indices.dim() == 2 and sparse_indices.shape[0] == T,
            f"sparse_indices must be [{T}, topk], got {tuple(sparse_indices.shape)}")
     _check(sparse_indices.dtype == torch.int32, "sparse_indices must be int32")
+    _check(int(num_splits) >= 0, f"num_splits must be >= 0, got {num_splits}")
     dev = q_nope.device
     _check(dev.type == "cuda", "tensors must live on a GPU device")
     for name, x in (("q_pe", q_pe), ("ckv_cache", ckv_cache), ("kpe_cache", kpe_cache),
@@ -84,7 +96,25 @@ def _attention(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, num
     q_pe = _inner_contiguous(q_pe)
     idx = _inner_contiguous(sparse_indices)
     K = idx.shape[1]
+    a = _lib.AttnArgs()
+    a.q_nope, a.q_nope_stride_t, a.q_nope_stride_h = q_nope.data_ptr(), q_nope.stride(0), q_nope.stride(1)
+    a.q_pe, a.q_pe_stride_t, a.q_pe_stride_h = q_pe.data_ptr(), q_pe.stride(0), q_pe.stride(1)
+    a.ckv, a.ckv_stride_page, a.ckv_stride_tok = ckv.data_ptr(), ckv_sp, ckv_so
+    a.kpe, a.kpe_stride_page, a.kpe_stride_tok = kpe.data_ptr(), kpe_sp, kpe_so
+    a.sparse_indices, a.idx_stride_t = idx.data_ptr(), idx.stride(0)
+    a.num_tokens, a.num_heads, a.topk = T, H, K
+    a.page_size, a.num_pages = ps, pages
+    a.head_dim_ckv, a.head_dim_kpe = HEAD_DIM_CKV, HEAD_DIM_KPE
+    a.sm_scale = float(sm_scale)
+    a.num_splits = int(num_splits)
+    return a, (q_nope, q_pe, ckv, kpe, idx), T, H, K, dev
 
+
+def _attention(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, num_splits: int,
+               output: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
+               workspace: Optional[torch.Tensor] = None):
+    a, keep, T, H, K, dev = _attn_args(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices,
+                                       sm_scale, num_splits)
     if output is None:
         output = torch.empty((T, H, HEAD_DIM_CKV), dtype=torch.bfloat16, device=dev)
     if lse is None:
@@ -94,27 +124,24 @@ def _attention(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, num
            "output must be a [T, H, 512] bfloat16 tensor with a contiguous last dim")
     _check(tuple(lse.shape) == (T, H) and lse.dtype == torch.float32 and lse.device == dev,
            "lse must be a [T, H] float32 tensor")
-
     lib = _lib.load()
     ws_bytes = lib.dsa_attn_workspace_bytes(T, H, K, int(num_splits))
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes else None
-
-    a = _lib.AttnArgs()
-    a.q_nope, a.q_nope_stride_t, a.q_nope_stride_h = q_nope.data_ptr(), q_nope.stride(0), q_nope.stride(1)
-    a.q_pe, a.q_pe_stride_t, a.q_pe_stride_h = q_pe.data_ptr(), q_pe.stride(0), q_pe.stride(1)
-    a.ckv, a.ckv_stride_page, a.ckv_stride_tok = ckv.data_ptr(), ckv_sp, ckv_so
-    a.kpe, a.kpe_stride_page, a.kpe_stride_tok = kpe.data_ptr(), kpe_sp, kpe_so
-    a.sparse_indices, a.idx_stride_t = idx.data_ptr(), idx.stride(0)
+    ws = None
+    if ws_bytes:
+        if workspace is not None:
+            _check(workspace.device == dev and workspace.is_contiguous()
+                   and workspace.numel() * workspace.element_size() >= ws_bytes,
+                   f"workspace must be a contiguous tensor of >= {ws_bytes} bytes on {dev}")
+            ws = workspace
+            ws_bytes = workspace.numel() * workspace.element_size()
+        else:
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     a.output, a.out_stride_t, a.out_stride_h = output.data_ptr(), output.stride(0), output.stride(1)
     a.lse, a.lse_stride_t, a.lse_stride_h = lse.data_ptr(), lse.stride(0), lse.stride(1)
-    a.num_tokens, a.num_heads, a.topk = T, H, K
-    a.page_size, a.num_pages = ps, pages
-    a.head_dim_ckv, a.head_dim_kpe = HEAD_DIM_CKV, HEAD_DIM_KPE
-    a.sm_scale = float(sm_scale)
-    a.num_splits = int(num_splits)
     a.workspace = ws.data_ptr() if ws is not None else None
     a.workspace_bytes = ws_bytes
     _lib.check("dsa_attn_fwd", lib.dsa_attn_fwd(ctypes.byref(a), _stream_handle(dev)))
+    del keep
     return output, lse
 
 
@@ -143,10 +170,66 @@ def kernel_splitk_v2(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scal
 
 
 def kernel_out(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, output, lse,
-               num_splits: int = 0):
-    """Destination-passing variant: writes into ``output`` and ``lse``."""
+               num_splits: int = 0, workspace: Optional[torch.Tensor] = None):
+    """Destination-passing variant: writes into ``output`` and ``lse``.
+
+    ``workspace`` (optional) comes from :func:`new_workspace`; by default one
+    is taken from the framework's caching allocator for the call."""
     _attention(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, int(num_splits),
-               output=output, lse=lse)
+               output=output, lse=lse, workspace=workspace)
+    return output, lse
+
+
+def kernel_partial(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale,
+                   num_splits: int = 0):
+    """Per-chunk partials without the merge (the split half of
+    ``kernel_splitk``, reference ``kernel.py:343-434``).
+
+    Returns ``(part_acc [T,S,H,512] fp32, part_ml [T,S,H,2] fp32)``: for chunk
+    s, ``part_ml[...,0]`` is a reference max m (log2 units), ``part_ml[...,1]``
+    the sum of ``2^(x*log2(e) - m)`` over the chunk's valid slots and
+    ``part_acc`` the matching weighted sum of ckv rows.  Partials of disjoint
+    slot sets (e.g. cache shards on different devices) concatenated along S
+    merge with :func:`merge_partials`."""
+    a, keep, T, H, K, dev = _attn_args(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices,
+                                       sm_scale, num_splits)
+    lib = _lib.load()
+    S = int(lib.dsa_attn_num_splits(T, H, K, int(num_splits)))
+    nbytes = lib.dsa_attn_partial_bytes(T, H, K, int(num_splits))
+    ws = torch.empty(max(nbytes // 4, 4), dtype=torch.float32, device=dev)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * 4
+    _lib.check("dsa_attn_fwd_partial", lib.dsa_attn_fwd_partial(ctypes.byref(a),
+                                                                _stream_handle(dev)))
+    del keep
+    n_acc = T * S * H * HEAD_DIM_CKV
+    return ws[:n_acc].view(T, S, H, HEAD_DIM_CKV), ws[n_acc:n_acc + T * S * H * 2].view(T, S, H, 2)
+
+
+def merge_partials(part_acc: torch.Tensor, part_ml: torch.Tensor,
+                   output: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None):
+    """Log-sum-exp merge of partials along S (reference ``kernel.py:437-493``);
+    returns ``(output [T,H,512] bf16, lse [T,H] fp32 base-2)``."""
+    _check(part_acc.dim() == 4 and part_acc.shape[-1] == HEAD_DIM_CKV
+           and part_acc.dtype == torch.float32, "part_acc must be [T, S, H, 512] float32")
+    T, S, H, _ = part_acc.shape
+    _check(tuple(part_ml.shape) == (T, S, H, 2) and part_ml.dtype == torch.float32,
+           f"part_ml must be [{T}, {S}, {H}, 2] float32")
+    _check(part_acc.device == part_ml.device and part_acc.device.type == "cuda",
+           "partials must live on one GPU device")
+    dev = part_acc.device
+    acc = part_acc.contiguous()
+    ml = part_ml.contiguous()
+    if output is None:
+        output = torch.empty((T, H, HEAD_DIM_CKV), dtype=torch.bfloat16, device=dev)
+    if lse is None:
+        lse = torch.empty((T, H), dtype=torch.float32, device=dev)
+    m = _lib.MergeArgs()
+    m.part_acc, m.part_ml = acc.data_ptr(), ml.data_ptr()
+    m.num_tokens, m.num_splits, m.num_heads = T, S, H
+    m.output, m.out_stride_t, m.out_stride_h = output.data_ptr(), output.stride(0), output.stride(1)
+    m.lse, m.lse_stride_t, m.lse_stride_h = lse.data_ptr(), lse.stride(0), lse.stride(1)
+    lib = _lib.load()
+    _lib.check("dsa_attn_merge", lib.dsa_attn_merge(ctypes.byref(m), _stream_handle(dev)))
     return output, lse
 
 

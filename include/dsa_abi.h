@@ -17,6 +17,8 @@
  *   dsa_indexer_topk      solution/triton/indexer_kernel.py:345-433
  *                         run_indexer_and_topk() (score kernel :4-287, top-k
  *                         kernel :289-343)
+ *   dsa_attn_fwd_partial  solution/triton/kernel.py:343-434  dsa_fwd_kernel_splitk
+ *   dsa_attn_merge        solution/triton/kernel.py:437-493  dsa_reduce_kernel
  *   dsa_attn_workspace_bytes / dsa_indexer_workspace_bytes
  *                         replace the per-call torch.zeros scratch of
  *                         kernel.py:526-528 and indexer_kernel.py:376-378
@@ -57,8 +59,10 @@ extern "C" {
  * and rows must be 16-byte aligned.  head_dim_ckv must be 512, head_dim_kpe
  * 64 and H a multiple of 16.  num_splits: 0 = automatic (fills the GPU),
  * otherwise the number of top-k chunks computed in parallel per token and
- * merged with log-sum-exp weights.  Split results are deterministic (no
- * atomics).
+ * merged with log-sum-exp weights in a fixed order (results are
+ * deterministic).  A split call needs dsa_attn_workspace_bytes() of workspace
+ * (16-byte aligned, contents irrelevant) for the fp32 partials; calls that run
+ * concurrently must not share a workspace.
  */
 typedef struct dsa_attn_args {
   const void *q_nope;
@@ -93,6 +97,47 @@ int32_t dsa_attn_num_splits(int64_t num_tokens, int64_t num_heads, int64_t topk,
 /* Workspace dsa_attn_fwd needs (0 when one split suffices). */
 size_t dsa_attn_workspace_bytes(int64_t num_tokens, int64_t num_heads, int64_t topk,
                                 int32_t requested_splits);
+
+/*
+ * The two halves of a split dsa_attn_fwd, for callers that merge partials
+ * themselves -- e.g. a cache sharded by slot ranges over several devices
+ * (each shard computes partials over its own slots, the partials are
+ * gathered, one dsa_attn_merge finishes) -- or that time the halves apart.
+ * Reference: the split partial kernel.py:343-434 and its merge
+ * kernel.py:437-493 (the separate launches of kernel_splitk, :534 and :555).
+ *
+ * dsa_attn_fwd_partial takes the same arguments as dsa_attn_fwd (output and
+ * lse are not touched and may be NULL) and writes, for every split count
+ * including 1, into the workspace (dsa_attn_partial_bytes() bytes):
+ *   part_acc = (float*)workspace              [T, S, H, 512]
+ *   part_ml  = part_acc + T*S*H*512           [T, S, H, 2]
+ * where for chunk s of token t and head h, with x_j the scaled logits of the
+ * chunk's valid slots: m = part_ml[...][0] is a reference value (in log2
+ * units) with every 2^(x_j*log2(e) - m) <= 256, l = part_ml[...][1] =
+ * sum_j 2^(x_j*log2(e) - m) and part_acc = sum_j 2^(x_j*log2(e) - m) *
+ * ckv[s_j].  A chunk without valid slots has m = -inf, l = 0, acc = 0.
+ *
+ * dsa_attn_merge combines num_splits such partials per (token, head) in
+ * split order: out = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s,
+ * lse = M + log2(sum_s 2^(m_s - M) l_s), M = max_s m_s (zeros / -inf when
+ * every chunk is empty).
+ */
+int dsa_attn_fwd_partial(const dsa_attn_args *args, void *stream);
+
+size_t dsa_attn_partial_bytes(int64_t num_tokens, int64_t num_heads, int64_t topk,
+                              int32_t requested_splits);
+
+typedef struct dsa_attn_merge_args {
+  const float *part_acc; /* [T, S, H, 512] fp32, 16-byte aligned */
+  const float *part_ml;  /* [T, S, H, 2] fp32 */
+  int64_t num_tokens, num_splits, num_heads;
+  void *output; /* [T, H, 512] bf16, element strides below */
+  int64_t out_stride_t, out_stride_h;
+  float *lse; /* [T, H] */
+  int64_t lse_stride_t, lse_stride_h;
+} dsa_attn_merge_args;
+
+int dsa_attn_merge(const dsa_attn_merge_args *args, void *stream);
 
 /*
  * Lightning indexer + top-k (indexer_kernel.py:345-433 interface; score

@@ -64,7 +64,9 @@ def test_split_choice():
     assert lib.dsa_attn_num_splits(64, 16, 2048, 16) == 16     # explicit request honoured
     assert lib.dsa_attn_num_splits(1, 16, 5, 128) == 5         # at most one key per split
     assert lib.dsa_attn_num_splits(4, 16, 0, 0) == 1
+    # fp32 partial outputs, then (max, sum) pairs
     assert lib.dsa_attn_workspace_bytes(64, 16, 2048, 0) == 64 * 4 * 16 * (512 + 2) * 4
+    assert lib.dsa_attn_workspace_bytes(256, 128, 2048, 2) == 256 * 2 * 128 * 514 * 4
     assert lib.dsa_attn_workspace_bytes(2048, 16, 2048, 0) == 0
 
 

@@ -17,7 +17,8 @@ import torch
 
 import oracle
 from conftest import LSE_ATOL, LSE_RTOL, OUT_ATOL, OUT_RTOL, mismatches
-from dsa_amd import kernel, kernel_out, kernel_splitk, kernel_splitk_v2, workloads
+from dsa_amd import (kernel, kernel_out, kernel_partial, kernel_splitk, kernel_splitk_v2,
+                     merge_partials, new_workspace, workloads)
 
 pytestmark = pytest.mark.gpu
 
@@ -182,7 +183,17 @@ def test_strided_inputs_and_dps_output():
     lse = torch.full((5, 16), float("nan"), dtype=torch.float32, device=DEV)
     kernel_out(qn, qp, g["ckv_cache"], g["kpe_cache"], idx, d["sm_scale"], out, lse)
     torch.cuda.synchronize()
-    _assert_parity(out.cpu(), lse.cpu(), *_oracle(d), "strided/DPS")
+    ref = _oracle(d)
+    _assert_parity(out.cpu(), lse.cpu(), *ref, "strided/DPS")
+    # caller-owned workspace, reused across calls (its contents do not matter)
+    ws = new_workspace(qn, 2048, num_splits=7)
+    ws.fill_(0xFF)
+    for _ in range(3):
+        out.fill_(float("nan"))
+        kernel_out(qn, qp, g["ckv_cache"], g["kpe_cache"], idx, d["sm_scale"], out, lse,
+                   num_splits=7, workspace=ws)
+        torch.cuda.synchronize()
+        _assert_parity(out.cpu(), lse.cpu(), *ref, "own workspace")
 
 
 def test_zero_tokens_and_zero_topk():
@@ -229,3 +240,38 @@ def test_large_logits_outlier_rows():
     out, lse = _run(kernel, d)
     _assert_parity(out, lse, *_oracle(d), "outliers")
     assert math.isfinite(float(lse.max()))
+
+
+def test_partials_merge_and_sharded_cache():
+    """kernel_partial + merge_partials == kernel; partials over two disjoint
+    slot shards (as two devices holding half the cache each would produce)
+    merge to the same result."""
+    d = workloads.cfg2(T=12, seed=21)
+    ref = _oracle(d)
+    g = workloads.to_device(d, DEV)
+    args = (g["q_nope"], g["q_pe"], g["ckv_cache"], g["kpe_cache"])
+    acc, ml = kernel_partial(*args, g["sparse_indices"], d["sm_scale"], num_splits=5)
+    assert acc.shape == (12, 5, 16, 512) and ml.shape == (12, 5, 16, 2)
+    out, lse = merge_partials(acc, ml)
+    torch.cuda.synchronize()
+    _assert_parity(out.cpu(), lse.cpu(), *ref, "partial+merge")
+    full_out, full_lse = kernel(*args, g["sparse_indices"], d["sm_scale"])
+    # shard by slot range: shard A owns slots < 65536, shard B the rest
+    idx = g["sparse_indices"]
+    lo = torch.where((idx >= 0) & (idx < 65536), idx, torch.full_like(idx, -1))
+    hi = torch.where(idx >= 65536, idx, torch.full_like(idx, -1))
+    pa = kernel_partial(*args, lo.contiguous(), d["sm_scale"], num_splits=1)
+    pb = kernel_partial(*args, hi.contiguous(), d["sm_scale"], num_splits=1)
+    out2, lse2 = merge_partials(torch.cat([pa[0], pb[0]], 1), torch.cat([pa[1], pb[1]], 1))
+    torch.cuda.synchronize()
+    _assert_parity(out2.cpu(), lse2.cpu(), *ref, "sharded merge")
+    assert torch.allclose(lse2, full_lse, atol=1e-4, rtol=0)
+    # an empty shard contributes nothing
+    none = torch.full_like(idx, -1)
+    pe = kernel_partial(*args, none, d["sm_scale"], num_splits=1)
+    torch.cuda.synchronize()
+    assert torch.isneginf(pe[1][..., 0]).all() and (pe[1][..., 1] == 0).all()
+    out3, lse3 = merge_partials(torch.cat([pa[0], pe[0], pb[0]], 1),
+                                torch.cat([pa[1], pe[1], pb[1]], 1))
+    torch.cuda.synchronize()
+    assert torch.equal(out3, out2) and torch.equal(lse3, lse2)
