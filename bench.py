@@ -43,7 +43,20 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="budget of the CPU-oracle baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run 5 plain device copies of BYTES bytes (the reference "
+                         "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     return ap.parse_args()
+
+
+def copy_calibration(nbytes: int) -> None:
+    import torch
+    src = torch.randint(0, 255, (nbytes,), dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": nbytes, "copies": 5}), flush=True)
 
 
 def load_traffic(config: str):
@@ -89,6 +102,9 @@ def cpu_baseline(d, budget_s: float):
 
 def main():
     a = parse()
+    if a.copy_calibration:
+        copy_calibration(a.copy_calibration)
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
         print(f"bench.py: this build measures one GPU only (asked for {max(a.gpus, world)}); "
