@@ -257,4 +257,74 @@ int dsa_attn_merge(const dsa_attn_merge_args *a, void *stream) {
   return ok();
 }
 
+// ---- indexer -------------------------------------------------------------
+
+namespace {
+constexpr int64_t kIndexerHeadDim = 128;
+constexpr int64_t kIndexerMaxHeads = 64;
+
+size_t up256(size_t x) { return (x + 255) / 256 * 256; }
+}  // namespace
+
+size_t dsa_indexer_workspace_bytes(int64_t num_tokens, int64_t num_heads, int64_t head_dim,
+                                   int64_t num_positions) {
+  if (num_tokens < 0 || num_heads < 0 || head_dim < 0 || num_positions < 0) return 0;
+  return up256((size_t)num_tokens * num_heads * 3 * head_dim) + up256((size_t)num_tokens * 4) +
+         up256((size_t)num_tokens * num_positions * 4);
+}
+
+int dsa_indexer_topk(const dsa_indexer_args *a, void *stream) {
+  const char *fn = "dsa_indexer_topk";
+  if (!a) return fail(DSA_EINVAL, "%s: args is NULL", fn);
+  if (a->head_dim != kIndexerHeadDim)
+    return fail(DSA_EUNSUPPORTED, "%s: head_dim must be 128 (got %lld)", fn, (long long)a->head_dim);
+  if (a->num_heads <= 0 || a->num_heads % 16 != 0 || a->num_heads > kIndexerMaxHeads)
+    return fail(DSA_EUNSUPPORTED, "%s: num_heads must be 16, 32, 48 or 64 (got %lld)", fn,
+                (long long)a->num_heads);
+  if (a->num_tokens < 0 || a->num_positions < 0 || a->topk < 0)
+    return fail(DSA_EINVAL, "%s: negative size", fn);
+  if (a->num_tokens > (1 << 24) || a->num_positions > 0x7fffffffLL || a->topk > (1 << 24) ||
+      a->num_tokens * a->num_positions > (1LL << 40))
+    return fail(DSA_EUNSUPPORTED, "%s: size beyond the supported range", fn);
+  if (a->num_tokens == 0) return ok();
+  if (!a->q_idx || !a->weights || !a->causal_limit || (a->topk > 0 && !a->out) ||
+      (a->num_positions > 0 && (!a->k_idx || !a->k_scale)))
+    return fail(DSA_EINVAL, "%s: NULL tensor pointer", fn);
+  if (!aligned(a->q_idx, 16) || !aligned(a->k_idx, 16) || !aligned(a->k_scale, 4) ||
+      !aligned(a->weights, 4) || !aligned(a->causal_limit, 4) || !aligned(a->out, 4) ||
+      !aligned(a->scores_out, 4))
+    return fail(DSA_EINVAL, "%s: misaligned pointer (e4m3 rows need 16 bytes)", fn);
+  if (a->block_table && (a->page_size <= 0 || a->block_table_stride < 0))
+    return fail(DSA_EINVAL, "%s: block_table needs page_size > 0 and a stride >= 0", fn);
+  const size_t pieces = up256((size_t)a->num_tokens * a->num_heads * 3 * kIndexerHeadDim);
+  const size_t flags = up256((size_t)a->num_tokens * 4);
+  const size_t scores = a->scores_out ? 0 : up256((size_t)a->num_tokens * a->num_positions * 4);
+  const size_t need = pieces + flags + scores;
+  if (!a->workspace || a->workspace_bytes < need || !aligned(a->workspace, 16))
+    return fail(DSA_EWORKSPACE, "%s: workspace of %zu bytes (16-byte aligned) needed, got %zu",
+                fn, need, a->workspace ? a->workspace_bytes : (size_t)0);
+
+  dsa::IndexerParams p = {};
+  p.q = a->q_idx;
+  p.k = a->k_idx;
+  p.k_scale = a->k_scale;
+  p.w = a->weights;
+  p.limit = a->causal_limit;
+  p.T = (int32_t)a->num_tokens;
+  p.Hi = (int32_t)a->num_heads;
+  p.S = (int32_t)a->num_positions;
+  p.topk = (int32_t)a->topk;
+  p.block_table = a->block_table;
+  p.bt_stride = a->block_table_stride;
+  p.page_size = (int32_t)(a->block_table ? a->page_size : 1);
+  p.out = a->out;
+  char *ws = static_cast<char *>(a->workspace);
+  p.q_pieces = reinterpret_cast<int8_t *>(ws);
+  p.q_flags = reinterpret_cast<int32_t *>(ws + pieces);
+  p.scores = a->scores_out ? a->scores_out : reinterpret_cast<float *>(ws + pieces + flags);
+  const hipError_t e = dsa::launch_indexer(p, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(DSA_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
+  return ok();
+}
+
 }  // extern "C"

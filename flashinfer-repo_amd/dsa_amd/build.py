@@ -22,6 +22,9 @@ HIPCC_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-shared",
+    # fused multiply-adds stay on, but `#pragma clang fp contract(off)` is
+    # honoured (the indexer score defines its rounding order)
+    "-ffp-contract=fast-honor-pragmas",
     # Packed-fp32 VALU forms are kept out of every code object.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]

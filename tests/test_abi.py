@@ -149,3 +149,40 @@ def test_workload_generators_shapes_and_padding():
     sel = workloads._distinct_below(1 << 17, 2048, torch.Generator().manual_seed(0))
     assert sel.unique().numel() == 2048 and int(sel.max()) < (1 << 17)
     assert np.isclose(workloads.SM_SCALE, 1 / np.sqrt(192))
+
+
+def _idx_args(**kw):
+    a = _lib.IndexerArgs()
+    base = dict(q_idx=0x1000, k_idx=0x2000, k_scale=0x3000, weights=0x4000, causal_limit=0x5000,
+                num_tokens=64, num_heads=64, head_dim=128, num_positions=32768, topk=2048,
+                block_table=None, block_table_stride=0, page_size=64, out=0x6000,
+                scores_out=None, workspace=0x8000,
+                workspace_bytes=_lib.load().dsa_indexer_workspace_bytes(64, 64, 128, 32768))
+    base.update(kw)
+    for k, v in base.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(head_dim=64), _lib.DSA_EUNSUPPORTED, "head_dim"),
+    (dict(num_heads=8), _lib.DSA_EUNSUPPORTED, "num_heads"),
+    (dict(num_heads=128), _lib.DSA_EUNSUPPORTED, "num_heads"),
+    (dict(topk=-1), _lib.DSA_EINVAL, "negative"),
+    (dict(q_idx=None), _lib.DSA_EINVAL, "NULL"),
+    (dict(out=None), _lib.DSA_EINVAL, "NULL"),
+    (dict(k_idx=0x2008), _lib.DSA_EINVAL, "misaligned"),
+    (dict(block_table=0x7000, page_size=0), _lib.DSA_EINVAL, "block_table"),
+    (dict(workspace_bytes=1024), _lib.DSA_EWORKSPACE, "workspace"),
+])
+def test_indexer_host_validation(kw, code, needle):
+    lib = _lib.load()
+    rc = lib.dsa_indexer_topk(ctypes.byref(_idx_args(**kw)), None)
+    assert rc == code and needle in lib.dsa_last_error().decode()
+
+
+def test_indexer_workspace_and_empty_call():
+    lib = _lib.load()
+    # q pieces (3 planes of int8) + per-token flags + fp32 scores, each 256-aligned
+    assert lib.dsa_indexer_workspace_bytes(64, 64, 128, 32768) == 64 * 64 * 3 * 128 + 256 + 64 * 32768 * 4
+    assert lib.dsa_indexer_topk(ctypes.byref(_idx_args(num_tokens=0, q_idx=None)), None) == 0
