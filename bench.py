@@ -31,6 +31,7 @@ sys.path[:0] = [ROOT, os.path.join(ROOT, "flashinfer-repo_amd")]
 METRIC = "µs/call + HBM GB/s & MFMA %, DSA decode H=16 topk=2048 T=64"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+INT8_PEAK_TOPS = 5000.0      # dense int8 MFMA (= the fp8 dense peak)
 GRAPH_CALLS = 20
 
 
@@ -39,7 +40,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="cfg2", choices=["cfg1", "cfg2", "cfg3", "cfg4"])
+    ap.add_argument("--config", default="cfg2", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"],
+                    help="cfg1-cfg4: sparse attention; cfg5: lightning indexer + top-k "
+                         "feeding the cfg2 attention")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="budget of the CPU-oracle baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -100,6 +103,154 @@ def cpu_baseline(d, budget_s: float):
                       f"{threads} threads, {el:.1f} s)"}
 
 
+def graph_of(fn, n):
+    """Capture n back-to-back calls of fn in one HIP graph (after an eager
+    warm-up on the capture-side stream, as torch's graph API expects)."""
+    import torch
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(n):
+            fn()
+    torch.cuda.synchronize()
+    return graph
+
+
+def time_graph(graph, n_per, steps, warmup):
+    """ms per call: warm-up replays, then HIP events around the replays (on
+    the current stream, which the kernels run on)."""
+    import torch
+    reps = max(1, -(-steps // n_per))
+    for _ in range(max(1, -(-warmup // n_per))):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / (reps * n_per), reps * n_per
+
+
+def time_eager(fn, steps):
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def cpu_indexer_baseline(d, budget_s: float):
+    """Times the CPU oracle's exact indexer score + top-k on a bounded sample
+    of the cfg5 rows (whole rows of all positions)."""
+    import numpy as np
+
+    import oracle
+    threads = min(16, os.cpu_count() or 1)
+    T = d["q_idx"].shape[0]
+    lim = d["causal_limit"].numpy().astype(np.int64)
+    qa, ka = d["q_idx"].numpy(), d["k_idx"].numpy()
+    sc, w = d["k_scale"].numpy(), d["weights"].numpy()
+    rows = 4
+    oracle.indexer_scores(qa[:1], ka, sc, w[:1], lim[:1], threads)  # warm-up
+    n, t0 = 0, time.perf_counter()
+    while True:
+        i = (n * rows) % T
+        s = oracle.indexer_scores(qa[i:i + rows], ka, sc, w[i:i + rows], lim[i:i + rows], threads)
+        oracle.topk(s, lim[i:i + rows], int(d["topk"]))
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n * rows >= 10 * T:
+            break
+    per_call = el / (n * rows) * T
+    return {"value": per_call * 1e6, "unit": "µs/call", "cores": threads, "kind": "port",
+            "sample": f"{n * rows} of {T} token rows (exact score over all positions + top-k, "
+                      f"OpenMP {threads} threads, {el:.1f} s), scaled to the {T}-row call"}
+
+
+def bench_indexer(a):
+    """cfg5: the lightning indexer + top-k (block-table slots) and the whole
+    indexer -> attention pipeline."""
+    import torch
+
+    from dsa_amd import kernel, workloads
+    from dsa_amd.indexer_kernel import run_indexer_and_topk
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    d = workloads.cfg5()
+    g = workloads.to_device(d, dev)
+    T, Hi, D = d["q_idx"].shape
+    S = d["k_idx"].shape[0]
+    K = int(d["topk"])
+    ia = (g["q_idx"], g["k_idx"], g["k_scale"], g["weights"], g["causal_limit"])
+    slots = run_indexer_and_topk(*ia, K, block_table=g["block_table"], page_size=64)
+    attn = (g["q_nope"], g["q_pe"], g["ckv_cache"], g["kpe_cache"])
+
+    def indexer():
+        run_indexer_and_topk(*ia, K, block_table=g["block_table"], page_size=64)
+
+    def scores_only():
+        run_indexer_and_topk(*ia, 0, return_scores=True)
+
+    def pipeline():
+        sl = run_indexer_and_topk(*ia, K, block_table=g["block_table"], page_size=64)
+        kernel(*attn, sl, d["sm_scale"])
+
+    per_graph = min(GRAPH_CALLS, a.steps)
+    ms_idx, timed_steps = time_graph(graph_of(indexer, per_graph), per_graph, a.steps, a.warmup)
+    ms_score, _ = time_graph(graph_of(scores_only, per_graph), per_graph, a.steps, a.warmup)
+    ms_pipe, _ = time_graph(graph_of(pipeline, per_graph), per_graph, a.steps, a.warmup)
+    eager_ms = time_eager(pipeline, a.steps)
+
+    ops = 2 * T * Hi * S * D                          # algorithmic dot-product ops
+    tops = ops / (ms_score * 1e-3) / 1e12
+    line = {
+        "metric": "µs/call, lightning indexer + top-k -> DSA attention (cfg5)",
+        "value": round(ms_pipe * 1e3, 3),
+        "unit": "µs/call",
+        "n_gpus": 1,
+        "steps": timed_steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_pipe, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8-e4m3 scores (exact), bf16 attention",
+        "data": "synthetic (seeded; q_idx,k_idx ~N(0,1) as e4m3, scale~U(0.5,2), w~N(0,1/8))",
+        "config": {"workload": f"cfg5: indexer T={T} heads={Hi} dim={D} positions={S} "
+                               f"top-{K} -> block-table slots -> cfg2 attention H=16",
+                   "timing": f"HIP graphs of {per_graph} back-to-back calls, replayed",
+                   "indexer_topk_us": round(ms_idx * 1e3, 3),
+                   "score_kernels_us": round(ms_score * 1e3, 3),
+                   "topk_kernel_us": round((ms_idx - ms_score) * 1e3, 3),
+                   "attention_us": round((ms_pipe - ms_idx) * 1e3, 3),
+                   "eager_pipeline_us": round(eager_ms * 1e3, 3)},
+        "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS,
+                     "unit": "TFLOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4),
+                     "traffic": None, "algorithmic_ops": ops,
+                     "kernel": "dsa_idx_prep_q_kernel + dsa_idx_score_kernel (timed via "
+                               "dsa_indexer_topk with topk=0)"},
+    }
+    del slots
+    if not a.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_indexer_baseline(d, a.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
 def main():
     a = parse()
     if a.copy_calibration:
@@ -111,6 +262,10 @@ def main():
               "the DSA path shards by tokens/heads with no exchange and is benchmarked at N=1.",
               file=sys.stderr)
         sys.exit(2)
+
+    if a.config == "cfg5":
+        bench_indexer(a)
+        return
 
     import torch
 
@@ -127,39 +282,6 @@ def main():
     alg_bytes = workloads.attention_bytes(d["sparse_indices"])
     alg_flops = workloads.attention_flops(d["sparse_indices"], H)
 
-    def graph_of(fn, n):
-        """Capture n back-to-back calls of fn in one HIP graph (after an eager
-        warm-up on the capture-side stream, as torch's graph API expects)."""
-        for _ in range(3):
-            fn()
-        torch.cuda.synchronize()
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            fn()
-        torch.cuda.current_stream().wait_stream(s)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            for _ in range(n):
-                fn()
-        torch.cuda.synchronize()
-        return graph
-
-    def time_graph(graph, n_per, steps, warmup):
-        """ms per call: warm-up replays, then HIP events around the replays
-        (on the current stream, which the kernels run on)."""
-        reps = max(1, -(-steps // n_per))
-        for _ in range(max(1, -(-warmup // n_per))):
-            graph.replay()
-        torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        for _ in range(reps):
-            graph.replay()
-        end.record()
-        torch.cuda.synchronize()
-        return start.elapsed_time(end) / (reps * n_per), reps * n_per
-
     per_graph = min(GRAPH_CALLS, a.steps)
     step_graph = graph_of(lambda: kernel(*args), per_graph)
     ms_per_step, timed_steps = time_graph(step_graph, per_graph, a.steps, a.warmup)
@@ -169,13 +291,7 @@ def main():
     ms_partial, _ = time_graph(part_graph, per_graph, a.steps, a.warmup)
 
     # eager (Python shim + ctypes + launches) for reference
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(a.steps):
-        kernel(*args)
-    end.record()
-    torch.cuda.synchronize()
-    eager_ms = start.elapsed_time(end) / a.steps
+    eager_ms = time_eager(lambda: kernel(*args), a.steps)
 
     us = ms_per_step * 1e3
     gbs = alg_bytes / (ms_partial * 1e-3) / 1e9          # dominant kernel

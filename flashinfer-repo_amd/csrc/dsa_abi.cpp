@@ -257,6 +257,8 @@ int dsa_attn_merge(const dsa_attn_merge_args *a, void *stream) {
   return ok();
 }
 
+}  // extern "C"
+
 // ---- indexer -------------------------------------------------------------
 
 namespace {
@@ -266,11 +268,32 @@ constexpr int64_t kIndexerMaxHeads = 64;
 size_t up256(size_t x) { return (x + 255) / 256 * 256; }
 }  // namespace
 
+namespace dsa {
+IndexerWorkspace indexer_workspace_layout(int64_t T, int64_t Hi, int64_t S, bool own_scores) {
+  IndexerWorkspace w = {};
+  const size_t kblocks = (size_t)(S + 15) / 16, qblocks = (size_t)T * (size_t)(Hi / 16);
+  size_t off = 0;
+  w.k_pieces = off;
+  off += up256(kblocks * 3 * 2 * 1024);
+  w.k_max = off;
+  off += up256(kblocks * 4);
+  w.q_pieces = off;
+  off += up256(qblocks * 3 * 2 * 1024);
+  w.q_max = off;
+  off += up256(qblocks * 4);
+  w.scores = off;
+  if (own_scores) off += up256((size_t)T * (size_t)S * 4);
+  w.total = off;
+  return w;
+}
+}  // namespace dsa
+
+extern "C" {
+
 size_t dsa_indexer_workspace_bytes(int64_t num_tokens, int64_t num_heads, int64_t head_dim,
                                    int64_t num_positions) {
   if (num_tokens < 0 || num_heads < 0 || head_dim < 0 || num_positions < 0) return 0;
-  return up256((size_t)num_tokens * num_heads * 3 * head_dim) + up256((size_t)num_tokens * 4) +
-         up256((size_t)num_tokens * num_positions * 4);
+  return dsa::indexer_workspace_layout(num_tokens, num_heads, num_positions, true).total;
 }
 
 int dsa_indexer_topk(const dsa_indexer_args *a, void *stream) {
@@ -296,13 +319,11 @@ int dsa_indexer_topk(const dsa_indexer_args *a, void *stream) {
     return fail(DSA_EINVAL, "%s: misaligned pointer (e4m3 rows need 16 bytes)", fn);
   if (a->block_table && (a->page_size <= 0 || a->block_table_stride < 0))
     return fail(DSA_EINVAL, "%s: block_table needs page_size > 0 and a stride >= 0", fn);
-  const size_t pieces = up256((size_t)a->num_tokens * a->num_heads * 3 * kIndexerHeadDim);
-  const size_t flags = up256((size_t)a->num_tokens * 4);
-  const size_t scores = a->scores_out ? 0 : up256((size_t)a->num_tokens * a->num_positions * 4);
-  const size_t need = pieces + flags + scores;
-  if (!a->workspace || a->workspace_bytes < need || !aligned(a->workspace, 16))
-    return fail(DSA_EWORKSPACE, "%s: workspace of %zu bytes (16-byte aligned) needed, got %zu",
-                fn, need, a->workspace ? a->workspace_bytes : (size_t)0);
+  const dsa::IndexerWorkspace lay = dsa::indexer_workspace_layout(
+      a->num_tokens, a->num_heads, a->num_positions, a->scores_out == nullptr);
+  if (!a->workspace || a->workspace_bytes < lay.total || !aligned(a->workspace, 256))
+    return fail(DSA_EWORKSPACE, "%s: workspace of %zu bytes (256-byte aligned) needed, got %zu",
+                fn, lay.total, a->workspace ? a->workspace_bytes : (size_t)0);
 
   dsa::IndexerParams p = {};
   p.q = a->q_idx;
@@ -319,9 +340,11 @@ int dsa_indexer_topk(const dsa_indexer_args *a, void *stream) {
   p.page_size = (int32_t)(a->block_table ? a->page_size : 1);
   p.out = a->out;
   char *ws = static_cast<char *>(a->workspace);
-  p.q_pieces = reinterpret_cast<int8_t *>(ws);
-  p.q_flags = reinterpret_cast<int32_t *>(ws + pieces);
-  p.scores = a->scores_out ? a->scores_out : reinterpret_cast<float *>(ws + pieces + flags);
+  p.k_pieces = reinterpret_cast<int8_t *>(ws + lay.k_pieces);
+  p.k_max = reinterpret_cast<int32_t *>(ws + lay.k_max);
+  p.q_pieces = reinterpret_cast<int8_t *>(ws + lay.q_pieces);
+  p.q_max = reinterpret_cast<int32_t *>(ws + lay.q_max);
+  p.scores = a->scores_out ? a->scores_out : reinterpret_cast<float *>(ws + lay.scores);
   const hipError_t e = dsa::launch_indexer(p, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(DSA_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
   return ok();

@@ -6,40 +6,54 @@
 //
 //   score[t,s] = sum_h w[t,h] * relu(q[t,h,:] . k[s,:] * k_scale[s])
 //
-// with one exact rounding order, so the GPU reproduces the CPU oracle bit for
-// bit: d = the exact dot of the e4m3fn values; a = fl32(fl32(d) * k_scale[s]);
-// r = max(a, 0); v = fl32(w[t,h] * r); heads are summed in blocks of 16, in
-// block order starting from 0, each block as (G0 + G1) + (G2 + G3) with
-// G = ((v0 + v1) + v2) + v3 over 4 consecutive heads.  Positions beyond
-// causal_limit[t] score -inf and are never selected.
+// computed in the factored form k_scale[s] * sum_h w[t,h] * relu(d[t,s,h])
+// (equal for a positive quantisation scale) with one exact rounding order, so
+// the GPU reproduces the CPU oracle bit for bit:
+//   D_h = d * 2^18, the exact integer dot of the values times 2^9;
+//   r_h = fl32(max(D_h, 0));
+//   the heads form 4 groups of Hi/4 consecutive heads; group g sums
+//   G_g = fma(w_h, r_h, G_g) over its heads in ascending order from 0;
+//   total = fl32(fl32(G_0 + G_1) + fl32(G_2 + G_3));
+//   score = fl32(total * c_s), c_s = fl32(k_scale[s] * 2^-18).
+// Positions beyond causal_limit[t] score -inf and are never selected.
 //
 // Exact dot on int8 MFMA.  Every finite e4m3fn value times 2^9 is an integer
 // x with |x| <= 229376 (18 bits); x = p0 + 2^7 p1 + 2^14 p2 with signed 7-bit
-// pieces (sign-magnitude split).  Then
-//   d * 2^18 = sum_{a,b} 2^(7(a+b)) sum_j pq_a[j] pk_b[j]
-// and each inner 128-term sum (|.| <= 128*127*127) is exact in the int32
-// accumulator of v_mfma_i32_16x16x64_i8.  For |value| < 32 the third piece is
-// zero and four piece products suffice; the combine is then exact in int32 when
-// |P11| < 2^16 and the one int32 -> fp32 conversion rounds like fl32(d)
-// (scaling by 2^-18 commutes with rounding; it is folded into k_scale).  Any
-// other case takes an exact fp64 combine.  e4m3fn NaN codes (0x7f, 0xff) count
-// as zero.
+// pieces (sign-magnitude split), so
+//   D = sum_{a,b} 2^(7(a+b)) sum_j pq_a[j] pk_b[j]
+// where each inner 128-term sum (|.| <= 128*127*127) is exact in the int32
+// accumulator of v_mfma_i32_16x16x64_i8.  When every |x| < 2^14 (values below
+// 32) the third piece is zero; four piece products remain, the two cross
+// products accumulate in one MFMA chain, and D = P00 + 2^7 X + 2^14 P11 is
+// combined in int32 when the operand maxima bound |D| below 2^31, else in
+// fp64.  Larger values take nine products and an fp64 combine (exact: every
+// partial sum stays below 2^50).  e4m3fn NaN codes (0x7f, 0xff) count as zero.
 //
 // Kernels:
-//   dsa_idx_prep_q_kernel  one workgroup per token: q codes -> piece planes
-//                          [T][Hi][3][128] int8 and the token's piece level.
-//   dsa_idx_score_kernel   one workgroup per (256 positions, token group): the
-//                          positions' k pieces stay in registers (B operands),
-//                          each token's q pieces are staged in LDS (double
-//                          buffered) and shared by the four waves.  Heads are
-//                          the MFMA M dimension, positions N.
-//   dsa_idx_topk_kernel    one workgroup per row: 4-pass radix select (8 bits
-//                          per pass) of the k-th largest order-preserving key,
-//                          then an ordered compaction that keeps every larger
-//                          score and the lowest positions among the ties, in
+//   dsa_idx_prep_kernel    q and k codes -> piece planes laid out as MFMA
+//                          operands in lane order (one 1 KB chunk per 16 rows,
+//                          piece and 64-wide k-step), plus the largest |x|
+//                          of every 16-row block.
+//   dsa_idx_score_kernel   one wave per query token, up to 8 tokens per
+//                          workgroup sharing a range of positions.  The
+//                          token's q pieces stay in registers (A operands,
+//                          heads as M); each 16-position block's k pieces are
+//                          one coalesced 1 KB load per operand (B, positions
+//                          as N).  No LDS and no barriers.
+//   dsa_idx_topk_kernel    one workgroup per row, the row in registers
+//                          (thread i owns a contiguous run of positions):
+//                          4-pass radix select (8 bits per pass, histograms
+//                          replicated 32 ways so equal digits do not collide
+//                          in one LDS bank) of the k-th largest order key,
+//                          then one packed scan that places every larger
+//                          score and the lowest positions among the ties in
 //                          ascending position order (reference intent:
 //                          indexer_kernel.py:289-343, strict '>' keeps the
 //                          earlier index).
+//   dsa_idx_topk_stream_kernel  the same selection re-reading the row from
+//                          memory, for rows longer than 65536 positions.
+#include <algorithm>
+
 #include "../../include/dsa_abi.h"
 #include "dsa_internal.h"
 
@@ -49,20 +63,17 @@ namespace {
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kIdxDim = 128;
-constexpr int kScoreSlots = 256;        // positions per score workgroup (4 waves x 4 x 16)
-constexpr int kSlotBlocks = 4;          // 16-position MFMA blocks per wave
-constexpr int kTokensPerGroup = 32;     // tokens one score workgroup walks
+constexpr int kChunk = 1024;              // one MFMA operand: 64 lanes x 16 bytes
+constexpr int kBlockBytes = 3 * 2 * kChunk;
+constexpr int kPrepThreads = 256;         // two 16-row blocks x 8 segments of 16 bytes
+constexpr int kScoreWaves = 8;            // tokens per score workgroup
+constexpr int kTargetScoreWaves = 2048;   // two waves per SIMD on 256 CUs
+constexpr int kMinBlocksPerWave = 8;
 constexpr int kTopkThreads = 1024;
-
-__device__ __forceinline__ void lds_dma16(const void *gsrc, void *ldst) {
-  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)gsrc,
-                                   (__attribute__((address_space(3))) void *)ldst, 16, 0, 0);
-}
-
-__device__ __forceinline__ void lds_dma4(const void *gsrc, void *ldst) {
-  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)gsrc,
-                                   (__attribute__((address_space(3))) void *)ldst, 4, 0, 0);
-}
+constexpr int kMaxRegEpt = 64;            // register top-k up to 1024 * 64 positions
+constexpr int kHistCopies = 32;
+constexpr int kHistPitch = 257;           // copy c of bin j at c*257 + j: bank (c + j) % 64
+constexpr int kTwoPieceLimit = 1 << 14;
 
 // e4m3fn code -> x = value * 2^9 (integer), NaN codes -> 0.
 __device__ __forceinline__ int e4m3_x(uint32_t c) {
@@ -79,218 +90,236 @@ __device__ __forceinline__ uint32_t piece_byte(int x, int pc) {
   return (uint32_t)(x < 0 ? -v : v) & 0xffu;
 }
 
-__device__ __forceinline__ int piece_level(int x) {
-  const int mag = x < 0 ? -x : x;
-  return mag >= (1 << 14) ? 2 : (mag >= (1 << 7) ? 1 : 0);
+__device__ __forceinline__ i32x4 load_chunk(const int8_t *p) { return *(const i32x4 *)p; }
+
+__device__ __forceinline__ i32x4 mfma(i32x4 a, i32x4 b, i32x4 c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
-// ---- q pieces ------------------------------------------------------------
+// ---- operand preparation -------------------------------------------------
+//
+// Row blocks 0 .. ceil(S/16)-1 are k blocks (16 positions); the following
+// T*Hi/16 blocks are q blocks (token t, heads 16j .. 16j+15).  Thread layout:
+// row r = (tid >> 3) & 15 of block (tid >> 7), 16-byte segment tid & 7.
+//
+// An operand chunk holds, for lane l = 16*g + c, the 16 bytes of k-step ks
+// (64 dims) starting at dim 16*g: of position 16*block + c (B operand), or of
+// the head that MFMA row c of head block hb stands for (A operand).  MFMA row
+// 4*g' + i of head block hb is head g'*Hi/4 + 4*hb + i, so that the four
+// output rows a lane receives (rows 4g'..4g'+3) are consecutive heads of the
+// lane's head group g'.
+__global__ __launch_bounds__(kPrepThreads) void dsa_idx_prep_kernel(IndexerParams p) {
+  __shared__ int s_max[2];
+  const int nkb = (p.S + 15) >> 4, nqb = p.Hi >> 4;
+  const int local = threadIdx.x >> 7;
+  const int rb = blockIdx.x * 2 + local;
+  const int r = (threadIdx.x >> 3) & 15, seg = threadIdx.x & 7;
+  const int total = nkb + p.T * nqb;
+  const bool active = rb < total;
+  const bool is_k = rb < nkb;
 
-__global__ __launch_bounds__(256) void dsa_idx_prep_q_kernel(IndexerParams p) {
-  __shared__ int s_level;
-  const int t = blockIdx.x;
-  if (threadIdx.x == 0) s_level = 0;
-  __syncthreads();
-  int level = 0;
-  const int chunks = p.Hi * (kIdxDim / 16);
-  for (int c = threadIdx.x; c < chunks; c += 256) {
-    const int h = c / (kIdxDim / 16), part = c % (kIdxDim / 16);
-    const uint4 raw = *(const uint4 *)(p.q + ((int64_t)t * p.Hi + h) * kIdxDim + part * 16);
-    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-    uint4 out[3];
-    uint32_t *o[3] = {&out[0].x, &out[1].x, &out[2].x};
-#pragma unroll
-    for (int pc = 0; pc < 3; ++pc)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uint32_t packed = 0;
-#pragma unroll
-        for (int b = 0; b < 4; ++b) packed |= piece_byte(e4m3_x((w[i] >> (8 * b)) & 0xff), pc) << (8 * b);
-        o[pc][i] = packed;
-      }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int b = 0; b < 4; ++b) level = max(level, piece_level(e4m3_x((w[i] >> (8 * b)) & 0xff)));
-    int8_t *dst = p.q_pieces + (((int64_t)t * p.Hi + h) * 3) * kIdxDim + part * 16;
-#pragma unroll
-    for (int pc = 0; pc < 3; ++pc) *(uint4 *)(dst + pc * kIdxDim) = out[pc];
+  uint4 raw = make_uint4(0, 0, 0, 0);
+  int t = 0, h = 0;
+  if (active) {
+    if (is_k) {
+      const int s = rb * 16 + r;
+      if (s < p.S) raw = *(const uint4 *)(p.k + (int64_t)s * kIdxDim + seg * 16);
+    } else {
+      const int qb = rb - nkb;
+      t = qb / nqb;
+      h = (qb % nqb) * 16 + r;
+      raw = *(const uint4 *)(p.q + ((int64_t)t * p.Hi + h) * kIdxDim + seg * 16);
+    }
   }
-  atomicMax(&s_level, level);
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  int xs[16];
+  int m = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    xs[i] = e4m3_x((w[i >> 2] >> (8 * (i & 3))) & 0xff);
+    m = max(m, xs[i] < 0 ? -xs[i] : xs[i]);
+  }
+  if (threadIdx.x < 2) s_max[threadIdx.x] = 0;
   __syncthreads();
-  if (threadIdx.x == 0) p.q_flags[t] = s_level;
+  atomicMax(&s_max[local], m);
+  __syncthreads();
+  if (!active) return;
+  const int bmax = s_max[local];
+
+  int8_t *dst;
+  int npieces;
+  const int ks = seg >> 2, g = seg & 3;
+  if (is_k) {
+    dst = p.k_pieces + (int64_t)rb * kBlockBytes + ks * kChunk + (16 * g + r) * 16;
+    npieces = bmax >= kTwoPieceLimit ? 3 : 2;  // the third plane is read only then
+    if (r == 0 && seg == 0) p.k_max[rb] = bmax;
+  } else {
+    const int quarter = p.Hi >> 2;
+    const int gq = h / quarter, within = h % quarter;
+    const int hb = within >> 2, row = 4 * gq + (within & 3);
+    dst = p.q_pieces + ((int64_t)t * nqb + hb) * kBlockBytes + ks * kChunk + (16 * g + row) * 16;
+    npieces = 3;
+    if (r == 0 && seg == 0) p.q_max[rb - nkb] = bmax;
+  }
+  for (int pc = 0; pc < npieces; ++pc) {
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t packed = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) packed |= piece_byte(xs[4 * i + b], pc) << (8 * b);
+      o[i] = packed;
+    }
+    *(uint4 *)(dst + pc * 2 * kChunk) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
 }
 
 // ---- scores --------------------------------------------------------------
 
-template <int NP>
-__device__ __forceinline__ void pair_products(const i32x4 (&aq)[2][3], const i32x4 (&kb)[2][3],
-                                              i32x4 (&P)[3][3]) {
-#pragma unroll
-  for (int a = 0; a < NP; ++a)
-#pragma unroll
-    for (int b = 0; b < NP; ++b) {
-      i32x4 c = {0, 0, 0, 0};
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) c = __builtin_amdgcn_mfma_i32_16x16x64_i8(aq[ks][a], kb[ks][b], c, 0, 0, 0);
-      P[a][b] = c;
-    }
+// (G0 + G1) + (G2 + G3) over the four 16-lane rows; every lane gets the sum.
+// permlane16_swap exchanges rows 0<->1 and 2<->3, permlane32_swap the two
+// halves; fp32 addition is commutative, so both lanes of a pair agree.
+__device__ __forceinline__ float sum_lane_groups(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const float s = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-__global__ __launch_bounds__(256, 1) void dsa_idx_score_kernel(IndexerParams p) {
-  // The score's rounding order is part of its definition: no fused
-  // multiply-adds.  The pragma covers only the operators written in this
-  // body (library helpers such as __fmul_rn are compiled under the global
-  // contraction setting and would fuse after inlining), so the products and
-  // sums below are plain operators.
+template <int NHB>
+__global__ __launch_bounds__(kScoreWaves * 64) void dsa_idx_score_kernel(IndexerParams p) {
+  // The rounding order is part of the score's definition: no contraction of
+  // the products and sums written below into fused multiply-adds (the one
+  // fused step of the definition is the explicit fmaf).
 #pragma clang fp contract(off)
-  // double-buffered q pieces of one token [64 heads max][3][128] + its weights
-  constexpr int kQBytes = 64 * 3 * kIdxDim;
-  __shared__ __attribute__((aligned(16))) int8_t lds_q[2][kQBytes];
-  __shared__ __attribute__((aligned(16))) float lds_w[2][64];
-
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int r16 = lane & 15, g = lane >> 4;
-  const int pos0 = blockIdx.x * kScoreSlots + wave * (kSlotBlocks * 16);
-  const int t_begin = blockIdx.y * kTokensPerGroup;
-  const int t_end = min(p.T, t_begin + kTokensPerGroup);
+  const int t = blockIdx.y * (blockDim.x >> 6) + wave;
+  const int nkb = (p.S + 15) >> 4;
+  const int b0 = blockIdx.x * p.blocks_per_wg;
+  const int b1 = min(nkb, b0 + p.blocks_per_wg);
+  if (t >= p.T || b0 >= b1) return;
+  const int col = lane & 15, g = lane >> 4;
+  const int lim = p.limit[t];
+  float *srow = p.scores + (int64_t)t * p.S;
 
-  // ---- this lane's k pieces (B operands) and scales, decoded once
-  i32x4 kb[kSlotBlocks][2][3];
-  float kscale[kSlotBlocks];
-  int klevel = 0;
+  int qmax = 0;
 #pragma unroll
-  for (int sb = 0; sb < kSlotBlocks; ++sb) {
-    const int s = pos0 + sb * 16 + r16;
-    const bool ok = s < p.S;
-    kscale[sb] = ok ? p.k_scale[s] * 0x1p-18f : 0.f;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      uint4 raw = make_uint4(0, 0, 0, 0);
-      if (ok) raw = *(const uint4 *)(p.k + (int64_t)s * kIdxDim + ks * 64 + g * 16);
-      const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-      for (int pc = 0; pc < 3; ++pc)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          uint32_t packed = 0;
-#pragma unroll
-          for (int b = 0; b < 4; ++b) packed |= piece_byte(e4m3_x((w[i] >> (8 * b)) & 0xff), pc) << (8 * b);
-          kb[sb][ks][pc][i] = (int)packed;
-        }
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int b = 0; b < 4; ++b) klevel = max(klevel, piece_level(e4m3_x((w[i] >> (8 * b)) & 0xff)));
-    }
-  }
-  // wave-uniform level of this wave's positions
-  klevel = __ballot(klevel == 2) ? 2 : (__ballot(klevel == 1) ? 1 : 0);
+  for (int j = 0; j < NHB; ++j) qmax = max(qmax, p.q_max[t * NHB + j]);
+  const bool q3 = qmax >= kTwoPieceLimit;
 
-  // ---- stage each token's q pieces (contiguous [Hi][3][128] bytes) and its
-  // head weights into LDS with global_load_lds (1 KB per instruction, split
-  // over the waves); the next token streams in while the current one is
-  // computed.
-  const int n_kb = p.Hi * 3 * kIdxDim / 1024;  // 1 KB DMA instructions per token
-  auto stage_token = [&](int tt, int bf) {
-    const int8_t *src = p.q_pieces + (int64_t)tt * p.Hi * 3 * kIdxDim;
-    for (int j = wave; j < n_kb; j += 4)
-      lds_dma16(src + j * 1024 + lane * 16, &lds_q[bf][j * 1024]);
-    if (wave == 0 && lane < p.Hi) lds_dma4(p.w + (int64_t)tt * p.Hi + lane, &lds_w[bf][0]);
-  };
-  if (t_begin < t_end) stage_token(t_begin, 0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-
-  for (int t = t_begin; t < t_end; ++t) {
-    const int buf = (t - t_begin) & 1;
-    if (t + 1 < t_end) stage_token(t + 1, buf ^ 1);
-    const int qlevel = p.q_flags[t];
-    const int level = max(qlevel, klevel);  // wave-uniform
-    const int8_t *qt = lds_q[buf];
-    const float *wt = lds_w[buf];
-
-    float z[4][kSlotBlocks];  // per head block: (G0 + G1) + (G2 + G3)
+  // A operands of this token: [head block][piece][k-step]
+  i32x4 qa[NHB][3][2];
+  const int8_t *qsrc = p.q_pieces + (int64_t)t * NHB * kBlockBytes + lane * 16;
 #pragma unroll
-    for (int hb = 0; hb < 4; ++hb) {
-      if (hb * 16 >= p.Hi) break;  // wave-uniform
-      i32x4 aq[2][3];
+  for (int hb = 0; hb < NHB; ++hb)
+#pragma unroll
+    for (int pc = 0; pc < 3; ++pc)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
+        qa[hb][pc][ks] = (pc < 2 || q3) ? load_chunk(qsrc + hb * kBlockBytes + (pc * 2 + ks) * kChunk)
+                                        : i32x4{0, 0, 0, 0};
+  // weights of the lane's rows: heads g*Hi/4 + 4*hb + i
+  float wl[NHB][4];
+  const float *wsrc = p.w + (int64_t)t * p.Hi + g * (p.Hi >> 2);
 #pragma unroll
-        for (int pc = 0; pc < 3; ++pc)
-          aq[ks][pc] = *(const i32x4 *)(qt + ((hb * 16 + r16) * 3 + pc) * kIdxDim + ks * 64 + g * 16);
-      const float4 wv = *(const float4 *)(wt + hb * 16 + 4 * g);
-      const float wh[4] = {wv.x, wv.y, wv.z, wv.w};
+  for (int hb = 0; hb < NHB; ++hb)
 #pragma unroll
-      for (int sb = 0; sb < kSlotBlocks; ++sb) {
-        i32x4 P[3][3];
-        float f[4];
-        if (level <= 1) {
-          pair_products<2>(aq, kb[sb], P);
-          bool small = true;
+    for (int i = 0; i < 4; ++i) wl[hb][i] = wsrc[4 * hb + i];
+
+  // pieces 0 and 1 of a block (the next block's are fetched one block ahead)
+  auto load_k01 = [&](int b, i32x4 (&kb)[2][2]) {
+    const int8_t *src = p.k_pieces + (int64_t)b * kBlockBytes + lane * 16;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) small &= (P[1][1][i] < (1 << 16)) && (P[1][1][i] > -(1 << 16));
-          if (__ballot(!small) == 0) {
-            // |D| < 2^31: exact in int32, one RNE conversion
+    for (int pc = 0; pc < 2; ++pc)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-              f[i] = (float)(P[0][0][i] + (P[0][1][i] + P[1][0][i]) * 128 + P[1][1][i] * 16384);
-          } else {
+      for (int ks = 0; ks < 2; ++ks) kb[pc][ks] = load_chunk(src + (pc * 2 + ks) * kChunk);
+  };
+  i32x4 kcur[2][2], knext[2][2];
+  load_k01(b0, kcur);
+
+  for (int b = b0; b < b1; ++b) {
+    const int s0 = b * 16;
+    if (s0 > lim) {  // every later position is masked as well
+      for (int bb = b; bb < b1; ++bb) {
+        const int s = bb * 16 + col;
+        if (g == 0 && s < p.S) srow[s] = -INFINITY;
+      }
+      break;
+    }
+    if (b + 1 < b1) load_k01(b + 1, knext);
+    const int kmax = p.k_max[b];
+    const int s = s0 + col;
+    const float cs = (s < p.S) ? p.k_scale[s] * 0x1p-18f : 0.f;
+    float G = 0.f;
+    if (!q3 && kmax < kTwoPieceLimit) {
+      const bool fits = (int64_t)qmax * kmax * kIdxDim < (1LL << 31);
+      i32x4 P00[NHB], X[NHB], P11[NHB];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const double D = (double)P[0][0][i] + 128.0 * (double)(P[0][1][i] + P[1][0][i]) +
-                               16384.0 * (double)P[1][1][i];
-              f[i] = (float)D;
-            }
-          }
-        } else {
-          pair_products<3>(aq, kb[sb], P);
+      for (int hb = 0; hb < NHB; ++hb) {
+        const i32x4 z = {0, 0, 0, 0};
+        P00[hb] = mfma(qa[hb][0][1], kcur[0][1], mfma(qa[hb][0][0], kcur[0][0], z));
+        X[hb] = mfma(qa[hb][0][0], kcur[1][0], z);
+        X[hb] = mfma(qa[hb][0][1], kcur[1][1], X[hb]);
+        X[hb] = mfma(qa[hb][1][0], kcur[0][0], X[hb]);
+        X[hb] = mfma(qa[hb][1][1], kcur[0][1], X[hb]);
+        P11[hb] = mfma(qa[hb][1][1], kcur[1][1], mfma(qa[hb][1][0], kcur[1][0], z));
+      }
+      if (fits) {
+#pragma unroll
+        for (int hb = 0; hb < NHB; ++hb)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            double D = 0.0;
-#pragma unroll
-            for (int a = 0; a < 3; ++a)
-#pragma unroll
-              for (int b = 0; b < 3; ++b) D += (double)P[a][b][i] * (double)(1 << (7 * (a + b)));
-            f[i] = (float)D;
+            const int D = (int)((uint32_t)P00[hb][i] + ((uint32_t)X[hb][i] << 7) +
+                                ((uint32_t)P11[hb][i] << 14));
+            G = __builtin_fmaf(wl[hb][i], (float)max(D, 0), G);
           }
-        }
-        // a = fl32(d32 * scale) (2^-18 folded into the scale); r = max(a, 0);
-        // v = fl32(w * r); G over this lane's 4 heads in order
-        float G = 0.f;
+      } else {
+#pragma unroll
+        for (int hb = 0; hb < NHB; ++hb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const double D = (double)P00[hb][i] + 128.0 * (double)X[hb][i] +
+                             16384.0 * (double)P11[hb][i];
+            G = __builtin_fmaf(wl[hb][i], (float)(D > 0.0 ? D : 0.0), G);
+          }
+      }
+    } else {
+      // nine products, grouped by the power 2^(7(a+b)) they carry
+      i32x4 kb[3][2];
+      const int8_t *src = p.k_pieces + (int64_t)b * kBlockBytes + lane * 16;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        kb[0][ks] = kcur[0][ks];
+        kb[1][ks] = kcur[1][ks];
+        kb[2][ks] = kmax >= kTwoPieceLimit ? load_chunk(src + (4 + ks) * kChunk) : i32x4{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int hb = 0; hb < NHB; ++hb) {
+        i32x4 C[5];
+#pragma unroll
+        for (int d = 0; d < 5; ++d) C[d] = i32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int a = 0; a < 3; ++a)
+#pragma unroll
+          for (int c = 0; c < 3; ++c)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) C[a + c] = mfma(qa[hb][a][ks], kb[c][ks], C[a + c]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float a = f[i] * kscale[sb];
-          const float r = a > 0.f ? a : 0.f;
-          const float v = wh[i] * r;
-          G = (i == 0) ? v : G + v;
+          const double D = (double)C[0][i] + 0x1p7 * (double)C[1][i] + 0x1p14 * (double)C[2][i] +
+                           0x1p21 * (double)C[3][i] + 0x1p28 * (double)C[4][i];
+          G = __builtin_fmaf(wl[hb][i], (float)(D > 0.0 ? D : 0.0), G);
         }
-        const float y = G + __shfl_xor(G, 16);
-        z[hb][sb] = y + __shfl_xor(y, 32);
       }
     }
-    float acc[kSlotBlocks];
+    const float total = sum_lane_groups(G);
+    const float score = total * cs;
+    if (g == 0 && s < p.S) srow[s] = (s > lim) ? -INFINITY : score;
 #pragma unroll
-    for (int sb = 0; sb < kSlotBlocks; ++sb) {
-      float a = 0.f;
+    for (int pc = 0; pc < 2; ++pc)
 #pragma unroll
-      for (int hb = 0; hb < 4; ++hb)
-        if (hb * 16 < p.Hi) a = a + z[hb][sb];
-      acc[sb] = a;
-    }
-    if (g == 0) {
-#pragma unroll
-      for (int sb = 0; sb < kSlotBlocks; ++sb) {
-        const int s = pos0 + sb * 16 + r16;
-        if (s < p.S) p.scores[(int64_t)t * p.S + s] = (s > p.limit[t]) ? -INFINITY : acc[sb];
-      }
-    }
-    // token t+1 landed, and every wave is done with buffer buf before the
-    // next iteration refills it
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+      for (int ks = 0; ks < 2; ++ks) kcur[pc][ks] = knext[pc][ks];
   }
 }
 
@@ -301,156 +330,268 @@ __device__ __forceinline__ uint32_t order_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Exclusive prefix sum over the 1024 threads of the block; returns the
-// exclusive sum and writes the total to *total.
-__device__ int block_exclusive_scan(int v, int *scratch, int *total) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(x, o);
-    if (lane >= o) x += y;
+__device__ __forceinline__ void emit_pos(const IndexerParams &p, int t, int32_t *out, int pos,
+                                         int rank) {
+  int v = pos;
+  if (p.block_table != nullptr) {
+    const int32_t page = p.block_table[(int64_t)t * p.bt_stride + pos / p.page_size];
+    v = page * p.page_size + pos % p.page_size;
   }
-  if (lane == 63) scratch[wave] = x;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int run = 0;
-    for (int w = 0; w < kTopkThreads / 64; ++w) {
-      const int c = scratch[w];
-      scratch[w] = run;
-      run += c;
-    }
-    scratch[kTopkThreads / 64] = run;
-  }
-  __syncthreads();
-  const int ex = scratch[wave] + x - v;
-  *total = scratch[kTopkThreads / 64];
-  __syncthreads();
-  return ex;
+  out[rank] = v;
 }
 
-__global__ __launch_bounds__(kTopkThreads) void dsa_idx_topk_kernel(IndexerParams p) {
-  __shared__ uint32_t hist[256];
-  __shared__ int scan_scratch[kTopkThreads / 64 + 1];
-  __shared__ uint32_t s_prefix, s_mask;
-  __shared__ int s_need;
+// Exclusive prefix sums of (a, b) over the 1024 threads of the block; the
+// totals go to *ta, *tb.
+__device__ int2 block_exclusive_scan2(int a, int b, int2 *scratch, int *ta, int *tb) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int x = a, y = b;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int xu = __shfl_up(x, o), yu = __shfl_up(y, o);
+    if (lane >= o) {
+      x += xu;
+      y += yu;
+    }
+  }
+  if (lane == 63) scratch[wave] = make_int2(x, y);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int ra = 0, rbv = 0;
+    for (int w = 0; w < kTopkThreads / 64; ++w) {
+      const int2 c = scratch[w];
+      scratch[w] = make_int2(ra, rbv);
+      ra += c.x;
+      rbv += c.y;
+    }
+    scratch[kTopkThreads / 64] = make_int2(ra, rbv);
+  }
+  __syncthreads();
+  const int2 base = scratch[wave];
+  *ta = scratch[kTopkThreads / 64].x;
+  *tb = scratch[kTopkThreads / 64].y;
+  __syncthreads();
+  return make_int2(base.x + x - a, base.y + y - b);
+}
 
+// After one pass's histogram is in tot[]: the digit that holds the
+// `need`-th largest key among those matching the prefix.  Run by wave 0.
+__device__ __forceinline__ void pick_digit(const uint32_t *tot, uint32_t prefix, uint32_t mask,
+                                           int shift, int need, uint32_t *s_prefix,
+                                           uint32_t *s_mask, int *s_need) {
+  const int l = threadIdx.x;  // 0..63, lane l owns bins 4l..4l+3
+  const uint32_t c0 = tot[4 * l], c1 = tot[4 * l + 1], c2 = tot[4 * l + 2], c3 = tot[4 * l + 3];
+  const uint32_t local = c0 + c1 + c2 + c3;
+  uint32_t x = local;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_down(x, o);
+    if (l + o < 64) x += y;
+  }
+  uint32_t cum = x - local;  // keys in the bins above this lane's
+  const uint32_t cs[4] = {c0, c1, c2, c3};
+#pragma unroll
+  for (int b = 3; b >= 0; --b) {
+    if ((int)cum < need && (int)(cum + cs[b]) >= need) {
+      *s_prefix = prefix | ((uint32_t)(4 * l + b) << shift);
+      *s_mask = mask | (255u << shift);
+      *s_need = need - (int)cum;
+    }
+    cum += cs[b];
+  }
+}
+
+// Shared state of one top-k workgroup.
+struct TopkShared {
+  uint32_t hist[kHistCopies * kHistPitch];
+  uint32_t tot[256];
+  int2 scan[kTopkThreads / 64 + 1];
+  uint32_t prefix, mask;
+  int need;
+};
+
+// Rows with at most topk candidates: every candidate, then -1.
+__device__ __forceinline__ bool take_all(const IndexerParams &p, int t, int32_t *out, int n) {
+  if (n > p.topk) return false;
+  for (int i = threadIdx.x; i < p.topk; i += kTopkThreads) {
+    if (i < n) emit_pos(p, t, out, i, i);
+    else out[i] = -1;
+  }
+  return true;
+}
+
+// One radix pass: histogram of the digit at `shift` over the keys matching
+// the prefix (everything else is counted in the spare bin 256 of each copy,
+// so the atomics need no branch), then the digit of the need-th largest.
+// for_keys(f) calls f(key, is_candidate) for each of this thread's keys.
+template <typename ForKeys>
+__device__ __forceinline__ void radix_pass(TopkShared &sh, int shift, ForKeys for_keys,
+                                           uint32_t &prefix, uint32_t &mask, int &need) {
+  for (int i = threadIdx.x; i < kHistCopies * kHistPitch; i += kTopkThreads) sh.hist[i] = 0;
+  __syncthreads();
+  uint32_t *myhist = sh.hist + (threadIdx.x & (kHistCopies - 1)) * kHistPitch;
+  const uint32_t pf = prefix, mk = mask;
+  for_keys([&](uint32_t key, bool cand) {
+    const uint32_t bin = (cand && (key & mk) == pf) ? ((key >> shift) & 255u) : 256u;
+    atomicAdd(&myhist[bin], 1u);
+  });
+  __syncthreads();
+  if (threadIdx.x < 256) {
+    uint32_t c = 0;
+#pragma unroll 8
+    for (int j = 0; j < kHistCopies; ++j) c += sh.hist[j * kHistPitch + threadIdx.x];
+    sh.tot[threadIdx.x] = c;
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) pick_digit(sh.tot, prefix, mask, shift, need, &sh.prefix, &sh.mask, &sh.need);
+  __syncthreads();
+  prefix = sh.prefix;
+  mask = sh.mask;
+  need = sh.need;
+}
+
+template <int EPT>
+__global__ __launch_bounds__(kTopkThreads) void dsa_idx_topk_kernel(IndexerParams p) {
+  static_assert(EPT <= 64, "selection masks are 64-bit");
+  __shared__ TopkShared sh;
   const int t = blockIdx.x;
   const float *row = p.scores + (int64_t)t * p.S;
   int32_t *out = p.out + (int64_t)t * p.topk;
   const int n = max(0, min(p.S, p.limit[t] + 1));  // candidates 0..n-1
-  const int K = p.topk;
+  if (take_all(p, t, out, n)) return;               // n > topk >= 1 below
 
-  auto emit = [&](int slot_pos, int rank) {
-    int v = slot_pos;
-    if (p.block_table != nullptr) {
-      const int32_t page = p.block_table[(int64_t)t * p.bt_stride + slot_pos / p.page_size];
-      v = page * p.page_size + slot_pos % p.page_size;
-    }
-    out[rank] = v;
-  };
-
-  if (n <= K) {
-    for (int i = threadIdx.x; i < K; i += kTopkThreads) {
-      if (i < n) emit(i, i);
-      else out[i] = -1;
-    }
-    return;
-  }
-
-  // ---- radix select of the K-th largest key
-  if (threadIdx.x == 0) {
-    s_prefix = 0;
-    s_mask = 0;
-    s_need = K;
-  }
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    if (threadIdx.x < 256) hist[threadIdx.x] = 0;
-    __syncthreads();
-    const uint32_t prefix = s_prefix, mask = s_mask;
-    for (int i = threadIdx.x; i < n; i += kTopkThreads) {
-      const uint32_t key = order_key(row[i]);
-      if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
-    }
-    __syncthreads();
-    if (threadIdx.x < 64) {
-      // lane l owns bins 4l..4l+3; suffix sums from the top bin down
-      const int l = threadIdx.x;
-      const uint32_t c0 = hist[4 * l], c1 = hist[4 * l + 1], c2 = hist[4 * l + 2], c3 = hist[4 * l + 3];
-      const uint32_t local = c0 + c1 + c2 + c3;
-      uint32_t above = 0;  // total of lanes > l
-      uint32_t x = local;
+  const int base = threadIdx.x * EPT;
+  const int nv = max(0, min(EPT, n - base));  // this thread's candidates
+  uint32_t key[EPT];
 #pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t y = __shfl_down(x, o);
-        if (l + o < 64) x += y;
-      }
-      above = x - local;
-      const int need = s_need;
-      // bins within this lane, from 4l+3 down
-      uint32_t cum = above;
-      const uint32_t cs[4] = {c0, c1, c2, c3};
-#pragma unroll
-      for (int b = 3; b >= 0; --b) {
-        if ((int)cum < need && (int)(cum + cs[b]) >= need) {
-          s_prefix = prefix | ((uint32_t)(4 * l + b) << shift);
-          s_mask = mask | (255u << shift);
-          s_need = need - (int)cum;
-        }
-        cum += cs[b];
-      }
-    }
-    __syncthreads();
-  }
-  const uint32_t tau = s_prefix;
-  const int need_eq = s_need;  // ties at tau to take, lowest positions first
+  for (int e = 0; e < EPT; ++e) key[e] = order_key(row[min(base + e, n - 1)]);
 
-  // ---- ordered compaction: thread i owns positions [i*chunk, (i+1)*chunk)
+  uint32_t prefix = 0, mask = 0;
+  int need = p.topk;
+  for (int shift = 24; shift >= 0; shift -= 8)
+    radix_pass(sh, shift,
+               [&](auto f) {
+#pragma unroll
+                 for (int e = 0; e < EPT; ++e) f(key[e], e < nv);
+               },
+               prefix, mask, need);
+  // prefix is now the k-th largest key; `need` of its ties are taken, lowest
+  // positions first.
+  uint64_t gt = 0, eq = 0;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    gt |= (uint64_t)(e < nv && key[e] > prefix) << e;
+    eq |= (uint64_t)(e < nv && key[e] == prefix) << e;
+  }
+  int tot_gt, tot_eq;
+  const int2 ex = block_exclusive_scan2(__builtin_popcountll(gt), __builtin_popcountll(eq), sh.scan,
+                                        &tot_gt, &tot_eq);
+  uint64_t sel = gt;
+  for (int left = need - ex.y; left > 0 && eq != 0; --left) {  // lowest ties first
+    sel |= eq & (~eq + 1);
+    eq &= eq - 1;
+  }
+  int o = ex.x + min(ex.y, need);
+  while (sel != 0) {
+    const int e = __builtin_ctzll(sel);
+    sel &= sel - 1;
+    emit_pos(p, t, out, base + e, o++);
+  }
+}
+
+// Rows longer than the register kernel holds: the same selection, reading
+// the row from memory in every pass.
+__global__ __launch_bounds__(kTopkThreads) void dsa_idx_topk_stream_kernel(IndexerParams p) {
+  __shared__ TopkShared sh;
+  const int t = blockIdx.x;
+  const float *row = p.scores + (int64_t)t * p.S;
+  int32_t *out = p.out + (int64_t)t * p.topk;
+  const int n = max(0, min(p.S, p.limit[t] + 1));
+  if (take_all(p, t, out, n)) return;
+
+  uint32_t prefix = 0, mask = 0;
+  int need = p.topk;
+  for (int shift = 24; shift >= 0; shift -= 8)
+    radix_pass(sh, shift,
+               [&](auto f) {
+                 for (int i = threadIdx.x; i < n; i += kTopkThreads) f(order_key(row[i]), true);
+               },
+               prefix, mask, need);
+  // ordered compaction: thread i owns positions [i*chunk, (i+1)*chunk)
   const int chunk = (n + kTopkThreads - 1) / kTopkThreads;
-  const int b0 = min(n, threadIdx.x * chunk), b1 = min(n, b0 + chunk);
+  const int c0 = min(n, (int)threadIdx.x * chunk), c1 = min(n, c0 + chunk);
   int n_gt = 0, n_eq = 0;
-  for (int i = b0; i < b1; ++i) {
+  for (int i = c0; i < c1; ++i) {
     const uint32_t key = order_key(row[i]);
-    n_gt += key > tau;
-    n_eq += key == tau;
+    n_gt += key > prefix;
+    n_eq += key == prefix;
   }
-  int tot;
-  const int eq_base = block_exclusive_scan(n_eq, scan_scratch, &tot);
-  const int take_eq = max(0, min(n_eq, need_eq - eq_base));
-  const int out_base = block_exclusive_scan(n_gt + take_eq, scan_scratch, &tot);
-  int o = out_base, eq_seen = 0;
-  for (int i = b0; i < b1; ++i) {
+  int tot_gt, tot_eq;
+  const int2 ex = block_exclusive_scan2(n_gt, n_eq, sh.scan, &tot_gt, &tot_eq);
+  int o = ex.x + min(ex.y, need);
+  int eq_left = need - ex.y;
+  for (int i = c0; i < c1; ++i) {
     const uint32_t key = order_key(row[i]);
-    bool sel = key > tau;
-    if (key == tau) {
-      sel = eq_seen < take_eq;
-      ++eq_seen;
+    bool sel = key > prefix;
+    if (key == prefix) {
+      sel = eq_left > 0;
+      --eq_left;
     }
-    if (sel) emit(i, o++);
+    if (sel) emit_pos(p, t, out, i, o++);
   }
-  for (int i = tot + threadIdx.x; i < K; i += kTopkThreads) out[i] = -1;
+}
+
+template <int NHB>
+hipError_t launch_score(const IndexerParams &p, dim3 grid, dim3 block, hipStream_t stream) {
+  hipLaunchKernelGGL(dsa_idx_score_kernel<NHB>, grid, block, 0, stream, p);
+  return hipGetLastError();
+}
+
+template <int EPT>
+hipError_t launch_topk(const IndexerParams &p, hipStream_t stream) {
+  hipLaunchKernelGGL(dsa_idx_topk_kernel<EPT>, dim3(p.T), dim3(kTopkThreads), 0, stream, p);
+  return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_indexer(const IndexerParams &p, hipStream_t stream) {
-  if (p.T == 0) return hipSuccess;
-  hipLaunchKernelGGL(dsa_idx_prep_q_kernel, dim3(p.T), dim3(256), 0, stream, p);
+hipError_t launch_indexer(const IndexerParams &pin, hipStream_t stream) {
+  if (pin.T == 0) return hipSuccess;
+  IndexerParams p = pin;
+  const int nkb = (p.S + 15) / 16, nqb = p.Hi / 16;
+  const int prep_blocks = (nkb + p.T * nqb + 1) / 2;
+  hipLaunchKernelGGL(dsa_idx_prep_kernel, dim3(prep_blocks), dim3(kPrepThreads), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (p.S > 0) {
-    const dim3 grid((p.S + kScoreSlots - 1) / kScoreSlots,
-                    (p.T + kTokensPerGroup - 1) / kTokensPerGroup);
-    hipLaunchKernelGGL(dsa_idx_score_kernel, grid, dim3(256), 0, stream, p);
-    e = hipGetLastError();
+    // tokens per workgroup (one wave each) and 16-position blocks per wave,
+    // aiming at two waves per SIMD with at least 8 blocks per wave
+    const int waves = std::min(p.T, kScoreWaves);
+    const int tgroups = (p.T + waves - 1) / waves;
+    int bx = (kTargetScoreWaves + waves * tgroups - 1) / (waves * tgroups);
+    bx = std::min(bx, (nkb + kMinBlocksPerWave - 1) / kMinBlocksPerWave);
+    bx = std::max(bx, 1);
+    p.blocks_per_wg = (nkb + bx - 1) / bx;
+    bx = (nkb + p.blocks_per_wg - 1) / p.blocks_per_wg;
+    const dim3 grid(bx, tgroups), block(64 * waves);
+    switch (nqb) {
+      case 1: e = launch_score<1>(p, grid, block, stream); break;
+      case 2: e = launch_score<2>(p, grid, block, stream); break;
+      case 3: e = launch_score<3>(p, grid, block, stream); break;
+      default: e = launch_score<4>(p, grid, block, stream); break;
+    }
     if (e != hipSuccess) return e;
   }
   if (p.topk > 0) {
-    hipLaunchKernelGGL(dsa_idx_topk_kernel, dim3(p.T), dim3(kTopkThreads), 0, stream, p);
-    e = hipGetLastError();
+    if (p.S <= kTopkThreads * 8) e = launch_topk<8>(p, stream);
+    else if (p.S <= kTopkThreads * 16) e = launch_topk<16>(p, stream);
+    else if (p.S <= kTopkThreads * 32) e = launch_topk<32>(p, stream);
+    else if (p.S <= kTopkThreads * kMaxRegEpt) e = launch_topk<kMaxRegEpt>(p, stream);
+    else {
+      hipLaunchKernelGGL(dsa_idx_topk_stream_kernel, dim3(p.T), dim3(kTopkThreads), 0, stream, p);
+      e = hipGetLastError();
+    }
   }
   return e;
 }
 
 }  // namespace dsa
-

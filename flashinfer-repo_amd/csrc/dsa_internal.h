@@ -53,6 +53,12 @@ hipError_t launch_attention(const AttnParams &p, hipStream_t stream);
 hipError_t launch_attention_partial(const AttnParams &p, hipStream_t stream);
 hipError_t launch_attention_merge(const AttnParams &p, hipStream_t stream);
 
+// Lightning indexer.  Workspace layout (see indexer_workspace_layout):
+//   k_pieces [ceil(S/16)][3 pieces][2 k-steps][1024 B]  MFMA B operands, lane order
+//   k_max    [ceil(S/16)]                               max |value * 2^9| per block
+//   q_pieces [T][Hi/16][3 pieces][2 k-steps][1024 B]    MFMA A operands, lane order
+//   q_max    [T][Hi/16]                                 max |value * 2^9| per 16 heads
+//   scores   [T][S] fp32                                (unless the caller's)
 struct IndexerParams {
   const uint8_t *q;       // [T][Hi][128] e4m3 codes
   const uint8_t *k;       // [S][128] e4m3 codes
@@ -65,9 +71,20 @@ struct IndexerParams {
   int32_t page_size;
   int32_t *out;           // [T][topk]
   float *scores;          // [T][S] (workspace or caller buffer)
-  int8_t *q_pieces;       // workspace: [T][Hi/16][3][16 heads][128] int8
-  int32_t *q_flags;       // workspace: [T] highest nonzero piece of q
+  int8_t *k_pieces;
+  int32_t *k_max;
+  int8_t *q_pieces;
+  int32_t *q_max;
+  int32_t blocks_per_wg;  // 16-position blocks one score workgroup walks (set by the launcher)
 };
+
+struct IndexerWorkspace {
+  size_t k_pieces, k_max, q_pieces, q_max, scores, total;  // byte offsets; total = size
+};
+
+// Offsets of the indexer's workspace regions; scores are left out when the
+// caller provides the score buffer.
+IndexerWorkspace indexer_workspace_layout(int64_t T, int64_t Hi, int64_t S, bool own_scores);
 
 hipError_t launch_indexer(const IndexerParams &p, hipStream_t stream);
 

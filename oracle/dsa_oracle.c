@@ -22,24 +22,25 @@
  *
  *   oracle_indexer_scores  the lightning-indexer score, whose structure follows
  *                          indexer_kernel.py:185-275 (dequantize -> dot -> ReLU
- *                          -> head weight -> sum over heads), with one exact
- *                          rounding order:
- *                            d   = sum_j q[t,h,j]*k[s,j]  (exact: fp8 products
- *                                  are exact and the 128-term sum spans < 53
- *                                  bits, so fp64 accumulation is exact)
- *                            d32 = fl32(d); a = fl32(d32*scale[s]);
- *                            r = max(a,0); v = fl32(w[t,h]*r);
- *                            score = fp32 sum over blocks of 16 heads in
- *                                    order, starting from 0; a block adds as
- *                                    (G0 + G1) + (G2 + G3) with
- *                                    Gg = ((v0 + v1) + v2) + v3 over heads
- *                                    16b+4g .. 16b+4g+3; no fused
- *                                    multiply-add.  (The reference's head sum,
- *                                    a Triton tl.sum, has no defined order;
- *                                    this one is fixed so the GPU can
- *                                    reproduce it bit for bit.)
- *                          Positions s > limit[t] are masked (-inf).  Hi must
- *                          be a multiple of 16.
+ *                          -> head weight -> sum over heads), in the factored
+ *                          form scale[s] * sum_h w[t,h]*relu(dot) (equal to
+ *                          sum_h w*relu(dot*scale) for a positive scale), with
+ *                          one exact rounding order:
+ *                            D   = 2^18 * sum_j q[t,h,j]*k[s,j]  (exact: fp8
+ *                                  products are exact and the 128-term sum
+ *                                  spans < 53 bits, so fp64 accumulation is
+ *                                  exact)
+ *                            r_h = fl32(max(D, 0))
+ *                            the heads form 4 groups of Hi/4 consecutive
+ *                            heads; G_g = fma(w[t,h], r_h, G_g) over group g's
+ *                            heads in ascending order, from G_g = 0
+ *                            total = fl32(fl32(G_0 + G_1) + fl32(G_2 + G_3))
+ *                            score = fl32(total * c_s),
+ *                                    c_s = fl32(scale[s] * 2^-18)
+ *                          (The reference's head sum, a Triton tl.sum, has no
+ *                          defined order; this one is fixed so that the GPU
+ *                          reproduces it bit for bit.)  Positions s > limit[t]
+ *                          are masked (-inf).  Hi must be a multiple of 16.
  *
  *   oracle_topk            top-k per row by (score desc, index asc), which is
  *                          what indexer_kernel.py:289-343 intends (strict '>'
@@ -217,31 +218,26 @@ int oracle_indexer_scores(const uint8_t *q, const uint8_t *k, const float *kscal
         scores[t * S + s] = -INFINITY;
         continue;
       }
-      float acc = 0.0f;
-      for (int64_t hb = 0; hb < Hi; hb += 16) {
-        float G[4];
-        for (int g = 0; g < 4; ++g) {
-          float gs = 0.0f;
-          for (int i = 0; i < 4; ++i) {
-            const int64_t h = hb + 4 * g + i;
-            const uint8_t *qh = q + (t * Hi + h) * D;
-            const uint8_t *ks = k + s * D;
-            double d = 0.0;
-            for (int64_t j = 0; j < D; ++j) d += (double)lut[qh[j]] * (double)lut[ks[j]];
-            volatile float d32 = (float)d;
-            volatile float a = d32 * kscale[s];
-            float r = a > 0.0f ? a : 0.0f;
-            volatile float v = w[t * Hi + h] * r;
-            gs = (i == 0) ? v : gs + v;
-          }
-          G[g] = gs;
+      const int64_t quarter = Hi / 4;
+      const uint8_t *ks = k + s * D;
+      float G[4];
+      for (int g = 0; g < 4; ++g) {
+        float acc = 0.0f;
+        for (int64_t h = g * quarter; h < (g + 1) * quarter; ++h) {
+          const uint8_t *qh = q + (t * Hi + h) * D;
+          double d = 0.0;
+          for (int64_t j = 0; j < D; ++j) d += (double)lut[qh[j]] * (double)lut[ks[j]];
+          const double dscaled = d * 262144.0; /* exact: a power of two */
+          const float r = (float)(dscaled > 0.0 ? dscaled : 0.0);
+          acc = fmaf(w[t * Hi + h], r, acc);
         }
-        volatile float b01 = G[0] + G[1];
-        volatile float b23 = G[2] + G[3];
-        volatile float blk = b01 + b23;
-        acc = acc + blk;
+        G[g] = acc;
       }
-      scores[t * S + s] = acc;
+      volatile float g01 = G[0] + G[1];
+      volatile float g23 = G[2] + G[3];
+      volatile float total = g01 + g23;
+      volatile float cs = kscale[s] * 0x1p-18f;
+      scores[t * S + s] = total * cs;
     }
   }
   return ORACLE_OK;

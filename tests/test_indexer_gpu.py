@@ -156,3 +156,36 @@ def test_cfg5_pipeline_end_to_end():
                                         NTHREADS)
     assert mismatches(out.float().cpu().numpy(), oracle.bf16_bits_to_f32(ref_out), OUT_ATOL, OUT_RTOL) == 0
     assert mismatches(lse.cpu().numpy(), ref_lse, LSE_ATOL, LSE_RTOL) == 0
+
+
+@pytest.mark.parametrize("S", [12000, 50000, 70000])
+def test_long_rows_every_topk_variant(S):
+    """Rows of 12000 / 50000 positions use the register top-k with 16 / 64
+    keys per thread; 70000 positions the streaming top-k."""
+    d = workloads.indexer_inputs(T=2, Hi=16, S=S, seed=S)
+    d["causal_limit"] = torch.tensor([S - 1, S // 2], dtype=torch.int32)
+    got_idx, got_sc = _gpu_indexer(d, 700)
+    ref_idx, ref_sc = _oracle(d, 700)
+    _assert_same(got_idx, got_sc, ref_idx, ref_sc, f"S={S}")
+
+
+def test_graph_replays_match_eager():
+    d = workloads.indexer_inputs(T=8, Hi=64, S=5000, seed=21)
+    g = workloads.to_device(d, DEV)
+    args = (g["q_idx"], g["k_idx"], g["k_scale"], g["weights"], g["causal_limit"])
+    eager = run_indexer_and_topk(*args, 256).clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run_indexer_and_topk(*args, 256)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = run_indexer_and_topk(*args, 256)
+    for _ in range(3):
+        out.fill_(-7)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        run_indexer_and_topk(*args, 100)   # eager work between replays
+        torch.cuda.synchronize()

@@ -15,6 +15,7 @@ Each check is chosen so a plausible slip (dropped q_pe.kpe term, natural-log
 lse, missing normalisation, transposed operand, wrong tie order) fails it.
 """
 import math
+from fractions import Fraction
 
 import numpy as np
 import pytest
@@ -182,10 +183,28 @@ def test_out_of_range_slot_raises():
 
 # ---------------------------------------------------------------- indexer
 
+def _f32_nearest_even(x: Fraction) -> np.float32:
+    """Exact rational -> nearest float32, ties to even (finite range)."""
+    f = np.float32(float(x))                      # within one ulp of the answer
+    cands = [np.nextafter(f, np.float32(-np.inf)), f, np.nextafter(f, np.float32(np.inf))]
+    best = None
+    for c in cands:
+        d = abs(Fraction(float(c)) - x)
+        even = (int(np.array(c, np.float32).view(np.uint32)) & 1) == 0
+        if best is None or d < best[0] or (d == best[0] and even):
+            best = (d, c)
+    return np.float32(best[1])
+
+
+def _fma32(a, b, c) -> np.float32:
+    return _f32_nearest_even(Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c)))
+
+
 def _exact_scores_independent(q, k, scale, w, limit):
     """Independent restatement: integer dot products (values x 2^9 are
     integers for every finite e4m3 code), then the documented fp32 rounding
-    sequence with numpy float32 scalars."""
+    sequence: exact-rational fma per head within four head groups, pairwise
+    group sum, then the scale."""
     tab = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(torch.float8_e4m3fn).double()
     tab = torch.nan_to_num(tab, nan=0.0).numpy()
     qi = np.round(tab[q] * 512).astype(np.int64)     # [T,Hi,D]
@@ -195,27 +214,33 @@ def _exact_scores_independent(q, k, scale, w, limit):
     dots = np.einsum("thd,sd->tsh", qi, ki)          # exact int64, = d * 2^18
     out = np.empty((T, S), np.float32)
     f = np.float32
+    quarter = Hi // 4
     for t in range(T):
         for s in range(S):
             if s > limit[t]:
                 out[t, s] = -np.inf
                 continue
-            acc = f(0.0)
-            for hb in range(0, Hi, 16):
-                G = []
-                for gi in range(4):
-                    gs = None
-                    for i in range(4):
-                        h = hb + 4 * gi + i
-                        d32 = f(float(dots[t, s, h]) * 2.0 ** -18)
-                        a = f(d32 * f(scale[s]))
-                        r = a if a > 0 else f(0.0)
-                        v = f(f(w[t, h]) * r)
-                        gs = v if gs is None else f(gs + v)
-                    G.append(gs)
-                acc = f(acc + f(f(G[0] + G[1]) + f(G[2] + G[3])))
-            out[t, s] = acc
+            G = []
+            for gi in range(4):
+                acc = f(0.0)
+                for h in range(gi * quarter, (gi + 1) * quarter):
+                    r = f(float(max(int(dots[t, s, h]), 0)))   # int -> fp32, one rounding
+                    acc = _fma32(w[t, h], r, acc)
+                G.append(acc)
+            total = f(f(G[0] + G[1]) + f(G[2] + G[3]))
+            out[t, s] = f(total * f(f(scale[s]) * f(2.0 ** -18)))
     return out, dots
+
+
+def test_fma32_helper_rounds_exactly():
+    # 1 + 2^-24 is a tie between 1 and 1 + 2^-23: to even (1.0); a fused
+    # product keeps the bits a separate multiply would drop
+    assert _f32_nearest_even(Fraction(1) + Fraction(1, 2 ** 24)) == np.float32(1.0)
+    assert _f32_nearest_even(Fraction(1) + Fraction(3, 2 ** 24)) == np.float32(1.0 + 2.0 ** -22)
+    a = np.float32(1.0 + 2.0 ** -12)
+    fused = _fma32(a, a, np.float32(-1.0))
+    assert fused == np.float32(2.0 ** -11 + 2.0 ** -24)
+    assert np.float32(np.float32(a * a) - np.float32(1.0)) != fused
 
 
 def _indexer_case(T, Hi, S, seed, dup_rows=0):
