@@ -41,17 +41,18 @@
 //                          one coalesced 1 KB load per operand (B, positions
 //                          as N).  No LDS and no barriers.
 //   dsa_idx_topk_kernel    one workgroup per row, the row in registers
-//                          (thread i owns a contiguous run of positions):
-//                          4-pass radix select (8 bits per pass, histograms
-//                          replicated 32 ways so equal digits do not collide
-//                          in one LDS bank) of the k-th largest order key,
-//                          then one packed scan that places every larger
-//                          score and the lowest positions among the ties in
-//                          ascending position order (reference intent:
-//                          indexer_kernel.py:289-343, strict '>' keeps the
-//                          earlier index).
+//                          (loaded coalesced, 1024-strided): 4-pass radix
+//                          select (8 bits per pass, histograms replicated 32
+//                          ways so equal digits do not collide in one LDS
+//                          bank) of the k-th largest order key; the keys then
+//                          move through LDS so that each thread owns a
+//                          contiguous run of positions, and one packed scan
+//                          places every larger score and the lowest positions
+//                          among the ties in ascending position order
+//                          (reference intent: indexer_kernel.py:289-343,
+//                          strict '>' keeps the earlier index).
 //   dsa_idx_topk_stream_kernel  the same selection re-reading the row from
-//                          memory, for rows longer than 65536 positions.
+//                          memory, for rows longer than 32768 positions.
 #include <algorithm>
 
 #include "../../include/dsa_abi.h"
@@ -70,7 +71,7 @@ constexpr int kScoreWaves = 8;            // tokens per score workgroup
 constexpr int kTargetScoreWaves = 2048;   // two waves per SIMD on 256 CUs
 constexpr int kMinBlocksPerWave = 8;
 constexpr int kTopkThreads = 1024;
-constexpr int kMaxRegEpt = 64;            // register top-k up to 1024 * 64 positions
+constexpr int kMaxRegEpt = 32;            // register top-k up to 1024 * 32 positions
 constexpr int kHistCopies = 32;
 constexpr int kHistPitch = 257;           // copy c of bin j at c*257 + j: bank (c + j) % 64
 constexpr int kTwoPieceLimit = 1 << 14;
@@ -109,7 +110,13 @@ __device__ __forceinline__ i32x4 mfma(i32x4 a, i32x4 b, i32x4 c) {
 // output rows a lane receives (rows 4g'..4g'+3) are consecutive heads of the
 // lane's head group g'.
 __global__ __launch_bounds__(kPrepThreads) void dsa_idx_prep_kernel(IndexerParams p) {
-  __shared__ int s_max[2];
+  __shared__ uint32_t lut[256];  // code -> signed piece bytes p0 | p1 << 8 | p2 << 16
+  __shared__ uint32_t s_max[2];  // largest magnitude code (code & 0x7f) of each row block
+  {
+    const int x = e4m3_x(threadIdx.x);
+    lut[threadIdx.x] = piece_byte(x, 0) | (piece_byte(x, 1) << 8) | (piece_byte(x, 2) << 16);
+  }
+  if (threadIdx.x < 2) s_max[threadIdx.x] = 0;
   const int nkb = (p.S + 15) >> 4, nqb = p.Hi >> 4;
   const int local = threadIdx.x >> 7;
   const int rb = blockIdx.x * 2 + local;
@@ -132,19 +139,17 @@ __global__ __launch_bounds__(kPrepThreads) void dsa_idx_prep_kernel(IndexerParam
     }
   }
   const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-  int xs[16];
-  int m = 0;
+  // e4m3 magnitudes order like their codes & 0x7f; the NaN code 0x7f ranks
+  // above 448, which only makes the block's bound conservative
+  uint32_t mc = 0;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    xs[i] = e4m3_x((w[i >> 2] >> (8 * (i & 3))) & 0xff);
-    m = max(m, xs[i] < 0 ? -xs[i] : xs[i]);
-  }
-  if (threadIdx.x < 2) s_max[threadIdx.x] = 0;
+  for (int i = 0; i < 16; ++i) mc = max(mc, (w[i >> 2] >> (8 * (i & 3))) & 0x7fu);
   __syncthreads();
-  atomicMax(&s_max[local], m);
+  atomicMax(&s_max[local], mc);
   __syncthreads();
   if (!active) return;
-  const int bmax = s_max[local];
+  const uint32_t top = s_max[local];
+  const int bmax = top == 0x7f ? (15 << 14) : e4m3_x(top);
 
   int8_t *dst;
   int npieces;
@@ -161,14 +166,17 @@ __global__ __launch_bounds__(kPrepThreads) void dsa_idx_prep_kernel(IndexerParam
     npieces = 3;
     if (r == 0 && seg == 0) p.q_max[rb - nkb] = bmax;
   }
+  uint32_t v[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) v[i] = lut[(w[i >> 2] >> (8 * (i & 3))) & 0xffu];
   for (int pc = 0; pc < npieces; ++pc) {
     uint32_t o[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int d = 0; d < 4; ++d) {
       uint32_t packed = 0;
 #pragma unroll
-      for (int b = 0; b < 4; ++b) packed |= piece_byte(xs[4 * i + b], pc) << (8 * b);
-      o[i] = packed;
+      for (int b = 0; b < 4; ++b) packed |= ((v[4 * d + b] >> (8 * pc)) & 0xffu) << (8 * b);
+      o[d] = packed;
     }
     *(uint4 *)(dst + pc * 2 * kChunk) = make_uint4(o[0], o[1], o[2], o[3]);
   }
@@ -186,39 +194,31 @@ __device__ __forceinline__ float sum_lane_groups(float v) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-template <int NHB>
-__global__ __launch_bounds__(kScoreWaves * 64) void dsa_idx_score_kernel(IndexerParams p) {
+// Scores of token t over the 16-position blocks [b0, b1).  NQP = pieces of
+// q in play (3 when the token holds a value of magnitude >= 32).
+template <int NHB, int NQP>
+__device__ __forceinline__ void score_range(const IndexerParams &p, int t, int b0, int b1, int qmax) {
   // The rounding order is part of the score's definition: no contraction of
   // the products and sums written below into fused multiply-adds (the one
   // fused step of the definition is the explicit fmaf).
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int t = blockIdx.y * (blockDim.x >> 6) + wave;
-  const int nkb = (p.S + 15) >> 4;
-  const int b0 = blockIdx.x * p.blocks_per_wg;
-  const int b1 = min(nkb, b0 + p.blocks_per_wg);
-  if (t >= p.T || b0 >= b1) return;
   const int col = lane & 15, g = lane >> 4;
   const int lim = p.limit[t];
   float *srow = p.scores + (int64_t)t * p.S;
-
-  int qmax = 0;
-#pragma unroll
-  for (int j = 0; j < NHB; ++j) qmax = max(qmax, p.q_max[t * NHB + j]);
-  const bool q3 = qmax >= kTwoPieceLimit;
+  uint32_t sh7;
+  asm volatile("s_mov_b32 %0, 7" : "=s"(sh7));
 
   // A operands of this token: [head block][piece][k-step]
-  i32x4 qa[NHB][3][2];
+  i32x4 qa[NHB][NQP][2];
   const int8_t *qsrc = p.q_pieces + (int64_t)t * NHB * kBlockBytes + lane * 16;
 #pragma unroll
   for (int hb = 0; hb < NHB; ++hb)
 #pragma unroll
-    for (int pc = 0; pc < 3; ++pc)
+    for (int pc = 0; pc < NQP; ++pc)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        qa[hb][pc][ks] = (pc < 2 || q3) ? load_chunk(qsrc + hb * kBlockBytes + (pc * 2 + ks) * kChunk)
-                                        : i32x4{0, 0, 0, 0};
+        qa[hb][pc][ks] = load_chunk(qsrc + hb * kBlockBytes + (pc * 2 + ks) * kChunk);
   // weights of the lane's rows: heads g*Hi/4 + 4*hb + i
   float wl[NHB][4];
   const float *wsrc = p.w + (int64_t)t * p.Hi + g * (p.Hi >> 2);
@@ -227,72 +227,77 @@ __global__ __launch_bounds__(kScoreWaves * 64) void dsa_idx_score_kernel(Indexer
 #pragma unroll
     for (int i = 0; i < 4; ++i) wl[hb][i] = wsrc[4 * hb + i];
 
-  // pieces 0 and 1 of a block (the next block's are fetched one block ahead)
-  auto load_k01 = [&](int b, i32x4 (&kb)[2][2]) {
+  // Blocks are fetched two ahead: pieces 0 and 1, the lane's scale, the
+  // block's magnitude bound.  Indices past the range are clamped so every
+  // step issues the same loads.
+  struct KBlock {
+    i32x4 k[2][2];
+    float cs;
+    int kmax;
+  };
+  auto fetch = [&](int b, KBlock &kb) {
+    b = min(b, b1 - 1);
     const int8_t *src = p.k_pieces + (int64_t)b * kBlockBytes + lane * 16;
 #pragma unroll
     for (int pc = 0; pc < 2; ++pc)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) kb[pc][ks] = load_chunk(src + (pc * 2 + ks) * kChunk);
+      for (int ks = 0; ks < 2; ++ks) kb.k[pc][ks] = load_chunk(src + (pc * 2 + ks) * kChunk);
+    kb.cs = p.k_scale[min(b * 16 + col, p.S - 1)];  // scaled by 2^-18 where it is used
+    kb.kmax = p.k_max[b];
   };
-  i32x4 kcur[2][2], knext[2][2];
-  load_k01(b0, kcur);
 
-  for (int b = b0; b < b1; ++b) {
-    const int s0 = b * 16;
-    if (s0 > lim) {  // every later position is masked as well
-      for (int bb = b; bb < b1; ++bb) {
-        const int s = bb * 16 + col;
-        if (g == 0 && s < p.S) srow[s] = -INFINITY;
-      }
-      break;
+  // the lane's group sum for its position -> the score, stored by lanes 0..15
+  auto finish = [&](float G, float cs, int s) {
+    const float total = sum_lane_groups(G);
+    const float score = total * (cs * 0x1p-18f);
+    if (g == 0 && s >= 0 && s < p.S) srow[s] = (s > lim) ? -INFINITY : score;
+  };
+  // int32 combine of one head block's products into the lane's group sum:
+  // D = ((P11 * 2^7 + X) * 2^7) + P00, two v_lshl_add_u32.  The shift amount
+  // is an opaque scalar so that the compiler keeps this nesting instead of
+  // redistributing the shifts into two shifts and an add3.
+  auto epilogue = [&](const i32x4 &P00, const i32x4 &X, const i32x4 &P11, int hb, float &G) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t hi = ((uint32_t)P11[i] << sh7) + (uint32_t)X[i];
+      const int D = (int)((hi << sh7) + (uint32_t)P00[i]);
+      G = __builtin_fmaf(wl[hb][i], (float)max(D, 0), G);
     }
-    if (b + 1 < b1) load_k01(b + 1, knext);
-    const int kmax = p.k_max[b];
-    const int s = s0 + col;
-    const float cs = (s < p.S) ? p.k_scale[s] * 0x1p-18f : 0.f;
+  };
+  auto two_piece = [&](const i32x4 (&kc)[2][2], int hb, i32x4 &P00, i32x4 &X, i32x4 &P11) {
+    const i32x4 z = {0, 0, 0, 0};
+    P00 = mfma(qa[hb][0][1], kc[0][1], mfma(qa[hb][0][0], kc[0][0], z));
+    X = mfma(qa[hb][0][0], kc[1][0], z);
+    X = mfma(qa[hb][0][1], kc[1][1], X);
+    X = mfma(qa[hb][1][0], kc[0][0], X);
+    X = mfma(qa[hb][1][1], kc[0][1], X);
+    P11 = mfma(qa[hb][1][1], kc[1][1], mfma(qa[hb][1][0], kc[1][0], z));
+  };
+
+  // fp64 combine (exact for every |D| < 2^53) of the general cases
+  auto general = [&](const KBlock &kc, int b, int s, bool two) {
     float G = 0.f;
-    if (!q3 && kmax < kTwoPieceLimit) {
-      const bool fits = (int64_t)qmax * kmax * kIdxDim < (1LL << 31);
-      i32x4 P00[NHB], X[NHB], P11[NHB];
+    if (NQP == 2 && two) {
 #pragma unroll
       for (int hb = 0; hb < NHB; ++hb) {
-        const i32x4 z = {0, 0, 0, 0};
-        P00[hb] = mfma(qa[hb][0][1], kcur[0][1], mfma(qa[hb][0][0], kcur[0][0], z));
-        X[hb] = mfma(qa[hb][0][0], kcur[1][0], z);
-        X[hb] = mfma(qa[hb][0][1], kcur[1][1], X[hb]);
-        X[hb] = mfma(qa[hb][1][0], kcur[0][0], X[hb]);
-        X[hb] = mfma(qa[hb][1][1], kcur[0][1], X[hb]);
-        P11[hb] = mfma(qa[hb][1][1], kcur[1][1], mfma(qa[hb][1][0], kcur[1][0], z));
-      }
-      if (fits) {
+        i32x4 P00, X, P11;
+        two_piece(kc.k, hb, P00, X, P11);
 #pragma unroll
-        for (int hb = 0; hb < NHB; ++hb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int D = (int)((uint32_t)P00[hb][i] + ((uint32_t)X[hb][i] << 7) +
-                                ((uint32_t)P11[hb][i] << 14));
-            G = __builtin_fmaf(wl[hb][i], (float)max(D, 0), G);
-          }
-      } else {
-#pragma unroll
-        for (int hb = 0; hb < NHB; ++hb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const double D = (double)P00[hb][i] + 128.0 * (double)X[hb][i] +
-                             16384.0 * (double)P11[hb][i];
-            G = __builtin_fmaf(wl[hb][i], (float)(D > 0.0 ? D : 0.0), G);
-          }
+        for (int i = 0; i < 4; ++i) {
+          const double D = (double)P00[i] + 128.0 * (double)X[i] + 16384.0 * (double)P11[i];
+          G = __builtin_fmaf(wl[hb][i], (float)(D > 0.0 ? D : 0.0), G);
+        }
       }
     } else {
-      // nine products, grouped by the power 2^(7(a+b)) they carry
-      i32x4 kb[3][2];
+      // all piece products, grouped by the power 2^(7(a+c)) they carry
+      i32x4 kb3[3][2];
       const int8_t *src = p.k_pieces + (int64_t)b * kBlockBytes + lane * 16;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        kb[0][ks] = kcur[0][ks];
-        kb[1][ks] = kcur[1][ks];
-        kb[2][ks] = kmax >= kTwoPieceLimit ? load_chunk(src + (4 + ks) * kChunk) : i32x4{0, 0, 0, 0};
+        kb3[0][ks] = kc.k[0][ks];
+        kb3[1][ks] = kc.k[1][ks];
+        kb3[2][ks] = kc.kmax >= kTwoPieceLimit ? load_chunk(src + (4 + ks) * kChunk)
+                                               : i32x4{0, 0, 0, 0};
       }
 #pragma unroll
       for (int hb = 0; hb < NHB; ++hb) {
@@ -300,11 +305,11 @@ __global__ __launch_bounds__(kScoreWaves * 64) void dsa_idx_score_kernel(Indexer
 #pragma unroll
         for (int d = 0; d < 5; ++d) C[d] = i32x4{0, 0, 0, 0};
 #pragma unroll
-        for (int a = 0; a < 3; ++a)
+        for (int a = 0; a < NQP; ++a)
 #pragma unroll
           for (int c = 0; c < 3; ++c)
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) C[a + c] = mfma(qa[hb][a][ks], kb[c][ks], C[a + c]);
+            for (int ks = 0; ks < 2; ++ks) C[a + c] = mfma(qa[hb][a][ks], kb3[c][ks], C[a + c]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const double D = (double)C[0][i] + 0x1p7 * (double)C[1][i] + 0x1p14 * (double)C[2][i] +
@@ -313,14 +318,64 @@ __global__ __launch_bounds__(kScoreWaves * 64) void dsa_idx_score_kernel(Indexer
         }
       }
     }
-    const float total = sum_lane_groups(G);
-    const float score = total * cs;
-    if (g == 0 && s < p.S) srow[s] = (s > lim) ? -INFINITY : score;
+    finish(G, kc.cs, s);
+  };
+
+  KBlock ka, kb, kc3;
+  fetch(b0, ka);
+  fetch(b0 + 1, kb);
+
+  // One block: prefetch block b+2 into `ahead`, then score block b from `kc`.
+  // Returns false once the rest of the range is causally masked.  The loop
+  // below is unrolled by three so that the three buffers keep fixed roles
+  // (a rotation by copies would wait for the loads just issued).
+  auto step = [&](int b, const KBlock &kc, KBlock &ahead) -> bool {
+    fetch(b + 2, ahead);  // unconditional: `ahead` then needs no merge of two versions
+    if (b * 16 > lim) {   // every later position is masked as well
+      for (int bb = b; bb < b1; ++bb) {
+        const int s = bb * 16 + col;
+        if (g == 0 && s < p.S) srow[s] = -INFINITY;
+      }
+      return false;
+    }
+    const int s = b * 16 + col;
+    const bool two = kc.kmax < kTwoPieceLimit;
+    const bool fits = (int64_t)qmax * kc.kmax * kIdxDim < (1LL << 31);
+    if constexpr (NQP == 2) {
+      if (two && fits) {
+        i32x4 P00[NHB], X[NHB], P11[NHB];
+        float G = 0.f;
 #pragma unroll
-    for (int pc = 0; pc < 2; ++pc)
+        for (int hb = 0; hb < NHB; ++hb) two_piece(kc.k, hb, P00[hb], X[hb], P11[hb]);
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) kcur[pc][ks] = knext[pc][ks];
+        for (int hb = 0; hb < NHB; ++hb) epilogue(P00[hb], X[hb], P11[hb], hb, G);
+        finish(G, kc.cs, s);
+        return true;
+      }
+    }
+    general(kc, b, s, two);
+    return true;
+  };
+  for (int b = b0; b < b1; b += 3) {
+    if (!step(b, ka, kc3) || b + 1 >= b1) break;
+    if (!step(b + 1, kb, ka) || b + 2 >= b1) break;
+    if (!step(b + 2, kc3, kb)) break;
   }
+}
+
+template <int NHB>
+__global__ __launch_bounds__(kScoreWaves * 64) void dsa_idx_score_kernel(IndexerParams p) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int t = blockIdx.y * (blockDim.x >> 6) + wave;
+  const int nkb = (p.S + 15) >> 4;
+  const int b0 = blockIdx.x * p.blocks_per_wg;
+  const int b1 = min(nkb, b0 + p.blocks_per_wg);
+  if (t >= p.T || b0 >= b1) return;
+  int qmax = 0;
+#pragma unroll
+  for (int j = 0; j < NHB; ++j) qmax = max(qmax, p.q_max[t * NHB + j]);
+  if (qmax >= kTwoPieceLimit) score_range<NHB, 3>(p, t, b0, b1, qmax);
+  else score_range<NHB, 2>(p, t, b0, b1, qmax);
 }
 
 // ---- top-k ---------------------------------------------------------------
@@ -400,9 +455,15 @@ __device__ __forceinline__ void pick_digit(const uint32_t *tot, uint32_t prefix,
   }
 }
 
-// Shared state of one top-k workgroup.
+// Shared state of one top-k workgroup.  After the radix passes the histogram
+// space holds the row's keys (KEYS of them, one pad word per 32) for the
+// ordered compaction.
+template <int KEYS>
 struct TopkShared {
-  uint32_t hist[kHistCopies * kHistPitch];
+  union {
+    uint32_t hist[kHistCopies * kHistPitch];
+    uint32_t keys[KEYS + KEYS / 32];
+  };
   uint32_t tot[256];
   int2 scan[kTopkThreads / 64 + 1];
   uint32_t prefix, mask;
@@ -423,8 +484,8 @@ __device__ __forceinline__ bool take_all(const IndexerParams &p, int t, int32_t 
 // the prefix (everything else is counted in the spare bin 256 of each copy,
 // so the atomics need no branch), then the digit of the need-th largest.
 // for_keys(f) calls f(key, is_candidate) for each of this thread's keys.
-template <typename ForKeys>
-__device__ __forceinline__ void radix_pass(TopkShared &sh, int shift, ForKeys for_keys,
+template <typename Shared, typename ForKeys>
+__device__ __forceinline__ void radix_pass(Shared &sh, int shift, ForKeys for_keys,
                                            uint32_t &prefix, uint32_t &mask, int &need) {
   for (int i = threadIdx.x; i < kHistCopies * kHistPitch; i += kTopkThreads) sh.hist[i] = 0;
   __syncthreads();
@@ -451,19 +512,18 @@ __device__ __forceinline__ void radix_pass(TopkShared &sh, int shift, ForKeys fo
 
 template <int EPT>
 __global__ __launch_bounds__(kTopkThreads) void dsa_idx_topk_kernel(IndexerParams p) {
-  static_assert(EPT <= 64, "selection masks are 64-bit");
-  __shared__ TopkShared sh;
+  static_assert(EPT <= 32, "selection masks and the LDS key stage hold 32 keys per thread");
+  __shared__ TopkShared<EPT * kTopkThreads> sh;
   const int t = blockIdx.x;
   const float *row = p.scores + (int64_t)t * p.S;
   int32_t *out = p.out + (int64_t)t * p.topk;
   const int n = max(0, min(p.S, p.limit[t] + 1));  // candidates 0..n-1
   if (take_all(p, t, out, n)) return;               // n > topk >= 1 below
 
-  const int base = threadIdx.x * EPT;
-  const int nv = max(0, min(EPT, n - base));  // this thread's candidates
+  // radix passes: key e of this thread is position e*1024 + tid (coalesced)
   uint32_t key[EPT];
 #pragma unroll
-  for (int e = 0; e < EPT; ++e) key[e] = order_key(row[min(base + e, n - 1)]);
+  for (int e = 0; e < EPT; ++e) key[e] = order_key(row[min(e * kTopkThreads + (int)threadIdx.x, n - 1)]);
 
   uint32_t prefix = 0, mask = 0;
   int need = p.topk;
@@ -471,28 +531,39 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_idx_topk_kernel(IndexerParam
     radix_pass(sh, shift,
                [&](auto f) {
 #pragma unroll
-                 for (int e = 0; e < EPT; ++e) f(key[e], e < nv);
+                 for (int e = 0; e < EPT; ++e) f(key[e], e * kTopkThreads + (int)threadIdx.x < n);
                },
                prefix, mask, need);
   // prefix is now the k-th largest key; `need` of its ties are taken, lowest
-  // positions first.
-  uint64_t gt = 0, eq = 0;
+  // positions first.  The keys move through LDS so that each thread then
+  // owns a contiguous run of positions [tid*EPT, tid*EPT + EPT).
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
-    gt |= (uint64_t)(e < nv && key[e] > prefix) << e;
-    eq |= (uint64_t)(e < nv && key[e] == prefix) << e;
+    const int pos = e * kTopkThreads + threadIdx.x;
+    sh.keys[pos + (pos >> 5)] = key[e];
+  }
+  __syncthreads();
+  const int base = threadIdx.x * EPT;
+  const int nv = max(0, min(EPT, n - base));
+  uint32_t gt = 0, eq = 0;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const int pos = base + e;
+    const uint32_t k = sh.keys[pos + (pos >> 5)];
+    gt |= (uint32_t)(e < nv && k > prefix) << e;
+    eq |= (uint32_t)(e < nv && k == prefix) << e;
   }
   int tot_gt, tot_eq;
-  const int2 ex = block_exclusive_scan2(__builtin_popcountll(gt), __builtin_popcountll(eq), sh.scan,
+  const int2 ex = block_exclusive_scan2(__builtin_popcount(gt), __builtin_popcount(eq), sh.scan,
                                         &tot_gt, &tot_eq);
-  uint64_t sel = gt;
+  uint32_t sel = gt;
   for (int left = need - ex.y; left > 0 && eq != 0; --left) {  // lowest ties first
     sel |= eq & (~eq + 1);
     eq &= eq - 1;
   }
   int o = ex.x + min(ex.y, need);
   while (sel != 0) {
-    const int e = __builtin_ctzll(sel);
+    const int e = __builtin_ctz(sel);
     sel &= sel - 1;
     emit_pos(p, t, out, base + e, o++);
   }
@@ -501,7 +572,7 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_idx_topk_kernel(IndexerParam
 // Rows longer than the register kernel holds: the same selection, reading
 // the row from memory in every pass.
 __global__ __launch_bounds__(kTopkThreads) void dsa_idx_topk_stream_kernel(IndexerParams p) {
-  __shared__ TopkShared sh;
+  __shared__ TopkShared<0> sh;
   const int t = blockIdx.x;
   const float *row = p.scores + (int64_t)t * p.S;
   int32_t *out = p.out + (int64_t)t * p.topk;
@@ -584,7 +655,6 @@ hipError_t launch_indexer(const IndexerParams &pin, hipStream_t stream) {
   if (p.topk > 0) {
     if (p.S <= kTopkThreads * 8) e = launch_topk<8>(p, stream);
     else if (p.S <= kTopkThreads * 16) e = launch_topk<16>(p, stream);
-    else if (p.S <= kTopkThreads * 32) e = launch_topk<32>(p, stream);
     else if (p.S <= kTopkThreads * kMaxRegEpt) e = launch_topk<kMaxRegEpt>(p, stream);
     else {
       hipLaunchKernelGGL(dsa_idx_topk_stream_kernel, dim3(p.T), dim3(kTopkThreads), 0, stream, p);
