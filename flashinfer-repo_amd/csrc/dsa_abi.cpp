@@ -184,6 +184,12 @@ int prepare_attn(const char *fn, const dsa_attn_args *a, bool partial_only, dsa:
   p->K = (int32_t)a->topk;
   p->page_size = (int32_t)a->page_size;
   p->num_slots = a->num_pages * a->page_size;
+  {
+    int sh = 0;
+    while ((int64_t(1) << sh) < a->page_size) ++sh;
+    p->ps_shift = sh;
+    p->ps_magic = (uint32_t)(((uint64_t)1 << (31 + sh)) / (uint64_t)a->page_size + 1);
+  }
   p->scale_log2 = a->sm_scale * 1.4426950408889634f;
   p->num_splits = S;
   p->chunk = chunk;

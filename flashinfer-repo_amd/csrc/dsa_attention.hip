@@ -11,14 +11,17 @@
 // over the valid slots s_j of sparse_indices[t] (-1 = padding).
 //
 // Work decomposition.  One workgroup = one (token, top-k chunk, block of
-// head groups).  Its waves share a 3-stage LDS ring of 32-key tiles: every
+// head groups).  Its waves share a 4-stage LDS ring of 32-key tiles: every
 // tile is gathered with global_load_lds_dwordx4 (16 B per lane straight into
 // LDS, no VGPR staging; one 1 KB ckv row per instruction, 8 kpe rows per
-// instruction), two tiles in flight while the third is consumed.  The gather
-// addresses of the chunk's keys and a valid-key mask per tile are staged in
-// LDS once, so issuing a tile's gathers never waits on an index load or a
-// division.  Padding keys gather a zero row, which keeps the number of loads
-// per wave and tile fixed and makes the vmcnt-based stage waits exact.
+// instruction), three tiles in flight while the fourth is consumed.  The
+// gather is latency-bound, so the ring depth (bytes in flight per CU) sets
+// the bandwidth; it uses the whole 160 KB of LDS.  The chunk's slot ids are
+// staged in LDS once (4 bytes per key, so no index load sits in front of a
+// gather; the page division is a multiply by a host-computed reciprocal) and
+// the valid-key mask of every tile is kept in one VGPR (lane i: tile i).
+// Padding keys gather a zero row, which keeps the number of loads per wave
+// and tile fixed and makes the vmcnt-based stage waits exact.
 //
 // Each wave belongs to one 16-head group and owns one slice of the 512 output
 // features.  Per tile:
@@ -81,12 +84,12 @@ constexpr int kCkvPitch = 1024 + 16;
 constexpr int kKpeGroupPitch = 1024 + 128;
 constexpr int kCkvStageBytes = kKeysPerTile * kCkvPitch;
 constexpr int kStageBytes = kCkvStageBytes + (kKeysPerTile / 8) * kKpeGroupPitch;
-constexpr int kStages = 3;
-constexpr int kAddrBytes = kMaxChunk * 8;                   // one row address per key
-constexpr int kMaskBytes = kMaxChunk / kKeysPerTile * 4;    // valid-key bits per tile
+constexpr int kStages = 4;
+constexpr int kSlotBytes = kMaxChunk * 4;                   // one slot id per key
 constexpr int kXchgBytes = 8 * 64 * 16;                     // one f32x4 per lane per wave
-constexpr int kLdsBytes = kStages * kStageBytes + 2 * kAddrBytes + kMaskBytes + kXchgBytes;
+constexpr int kLdsBytes = kStages * kStageBytes + kSlotBytes + kXchgBytes;
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one gfx950 CU");
+static_assert(kMaxChunk / kKeysPerTile <= 64, "one mask lane per tile");
 
 // The running max is only moved (and the accumulator rescaled) when a head's
 // scores exceed it by more than this many log2 units, so probabilities stay
@@ -188,10 +191,8 @@ template <int W, int FS>
 __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) {
   using R = Ring<W, FS>;
   __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
-  uint64_t *ckv_rows = (uint64_t *)(lds + kStages * kStageBytes);
-  uint64_t *kpe_rows = ckv_rows + kMaxChunk;
-  uint32_t *tile_mask = (uint32_t *)(kpe_rows + kMaxChunk);
-  f32x4 *xbuf = (f32x4 *)(lds + kStages * kStageBytes + 2 * kAddrBytes + kMaskBytes);
+  int32_t *slots = (int32_t *)(lds + kStages * kStageBytes);  // -1: padding / invalid
+  f32x4 *xbuf = (f32x4 *)(lds + kStages * kStageBytes + kSlotBytes);
 
   const int t = blockIdx.x / p.num_splits;
   const int split = blockIdx.x - t * p.num_splits;
@@ -211,9 +212,8 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
   const int n_keys = max(0, min(p.K, k_begin + p.chunk) - k_begin);
   const int n_tiles = (n_keys + kKeysPerTile - 1) / kKeysPerTile;
 
-  // ---- stage the gather addresses of the chunk's keys (padding and invalid
-  // ids -> the zero row) and one valid-key mask per tile; all index loads are
-  // issued before the first store so they overlap
+  // ---- stage the chunk's slot ids (padding and out-of-range ids -> -1);
+  // all index loads are issued before the first store so they overlap
   {
     constexpr int kPer = kMaxChunk / (W * 64);
     const int32_t *src = p.idx + (int64_t)t * p.idx_st + k_begin;
@@ -223,25 +223,12 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
       const int i = threadIdx.x + k * W * 64;
       sv[k] = i < n_keys ? src[i] : -1;
     }
-    const uint64_t zero_row = (uint64_t)(const char *)g_zero_row;
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
       const int i = threadIdx.x + k * W * 64;
       const int s = sv[k];
       const bool valid = s >= 0 && (int64_t)s < p.num_slots;
-      uint64_t ca = zero_row, ka = zero_row;
-      if (valid) {
-        const uint32_t pg = (uint32_t)s / (uint32_t)p.page_size;
-        const uint32_t of = (uint32_t)s - pg * (uint32_t)p.page_size;
-        ca = (uint64_t)(p.ckv + (int64_t)pg * p.ckv_sp + (int64_t)of * p.ckv_so);
-        ka = (uint64_t)(p.kpe + (int64_t)pg * p.kpe_sp + (int64_t)of * p.kpe_so);
-      }
-      const uint64_t bits = __ballot(valid);  // lanes 0-31: tile i/32, 32-63: the next
-      if (i < n_tiles * kKeysPerTile) {
-        ckv_rows[i] = ca;
-        kpe_rows[i] = ka;
-        if ((lane & 31) == 0) tile_mask[i / kKeysPerTile] = (uint32_t)(bits >> (lane & 32));
-      }
+      if (i < n_tiles * kKeysPerTile) slots[i] = valid ? s : -1;
     }
   }
 
@@ -263,18 +250,33 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
   // its own bookkeeping has nothing outstanding when the gather ring starts
   // and it adds no drain at the loop header.
   __builtin_amdgcn_s_waitcnt(0x0F70);
-  __syncthreads();  // addresses and masks visible; nothing gathered yet
+  __syncthreads();  // slot ids visible; nothing gathered yet
+
+  // valid-key mask of tile i in lane i (wave-uniform reads with readlane)
+  uint32_t tile_masks = 0;
+  for (int k = 0; 2 * k < n_tiles; ++k) {
+    const int i = k * 64 + lane;
+    const uint64_t bits = __ballot(i < n_tiles * kKeysPerTile && slots[i] >= 0);
+    tile_masks = lane == 2 * k ? (uint32_t)bits : tile_masks;
+    tile_masks = lane == 2 * k + 1 ? (uint32_t)(bits >> 32) : tile_masks;
+  }
 
   // ---- gather issue: this wave's share of tile j into stage j % kStages.
   // Lane l owns key 8*grp + (l & 7) of the tile, grp being the kpe group
   // (8 rows) this wave gathers (a half group when W == 8).
   const int grp = (W == 4) ? wave : (wave >> 1);
   const int row0 = (W == 4) ? 0 : 4 * (wave & 1);  // first ckv row within the group
+  const uint64_t zero_row = (uint64_t)(const char *)g_zero_row;
   auto issue_tile = [&](int j) {
     char *st = lds + (j % kStages) * kStageBytes;
-    const int key = j * kKeysPerTile + grp * 8 + (lane & 7);
-    const uint64_t ckv_addr = ckv_rows[key];
-    const uint64_t kpe_addr = kpe_rows[key];
+    const int sl = slots[j * kKeysPerTile + grp * 8 + (lane & 7)];
+    uint64_t ckv_addr = zero_row, kpe_addr = zero_row;
+    if (sl >= 0) {
+      const uint32_t pg = (uint32_t)(((uint64_t)(uint32_t)sl * p.ps_magic) >> (31 + p.ps_shift));
+      const uint32_t of = (uint32_t)sl - pg * (uint32_t)p.page_size;
+      ckv_addr = (uint64_t)(p.ckv + (int64_t)pg * p.ckv_sp + (int64_t)of * p.ckv_so);
+      kpe_addr = (uint64_t)(p.kpe + (int64_t)pg * p.kpe_sp + (int64_t)of * p.kpe_so);
+    }
 #pragma unroll
     for (int m = 0; m < R::kRows; ++m) {
       const char *src = (const char *)readlane64(ckv_addr, row0 + m) + lane * 16;
@@ -291,23 +293,10 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
   float m_run = -INFINITY;  // reference max of x*log2(e) for this lane's head
   float l_run = 0.f;        // running sum over this lane's keys (reduced at the end)
 
-  const int pre = min(n_tiles, kStages - 1);
-  for (int j = 0; j < pre; ++j) issue_tile(j);
-
-  for (int i = 0; i < n_tiles; ++i) {
-    if (i + 1 < n_tiles)
-      wait_vmcnt<R::kLoads>();  // tile i+1 may stay in flight
-    else
-      wait_vmcnt<0>();
-    __builtin_amdgcn_s_barrier();  // every wave's share of tile i landed; tile i-1 consumed
-    if (i + kStages - 1 < n_tiles) issue_tile(i + kStages - 1);
-
-    const char *st_ckv = lds + (i % kStages) * kStageBytes;
+  // ---- per-tile stages, shared by both loop shapes below
+  // S^T partial (or, FS == 1, complete) of the wave's key blocks and k-steps
+  auto scores = [&](const char *st_ckv, f32x4 (&sacc)[2]) {
     const char *st_kpe = st_ckv + kCkvStageBytes;
-    const uint32_t vmask = tile_mask[i];
-
-    // ---- S^T = K . Q^T (this wave's blocks and k-steps)
-    f32x4 sacc[2];
 #pragma unroll
     for (int bb = 0; bb < R::kBlocks; ++bb) {
       const int b = qb0 + bb;
@@ -316,27 +305,26 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
       const char *kp = st_kpe + (kk >> 3) * kKpeGroupPitch + (kk & 7) * 16;
       sacc[bb] = qk_part<R::kParts>(part, rowp, kp, qreg, g);
     }
-    if (FS >= 2) {
-      // partial scores of the group's waves, added in a fixed order
-      xbuf[wave * 64 + lane] = sacc[0];
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): partial written
-      __builtin_amdgcn_s_barrier();
-      const int base = hg * FS;
+  };
+  // the group's partial S^T, added in a fixed order (after the exchange)
+  auto reduce = [&](f32x4 (&sacc)[2]) {
+    const int base = hg * FS;
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        f32x4 c = xbuf[(base + b) * 64 + lane];
+    for (int b = 0; b < 2; ++b) {
+      f32x4 c = xbuf[(base + b) * 64 + lane];
 #pragma unroll
-        for (int pp = 1; pp < R::kParts; ++pp) c += xbuf[(base + b + 2 * pp) * 64 + lane];
-        sacc[b] = c;
-      }
+      for (int pp = 1; pp < R::kParts; ++pp) c += xbuf[(base + b + 2 * pp) * 64 + lane];
+      sacc[b] = c;
     }
-
+  };
+  const int kbase = (g & 1) * 8 + (g >> 1);
+  // online softmax of one tile -> its probabilities (bf16 hi + lo parts)
+  auto softmax = [&](const f32x4 (&sacc)[2], uint32_t vmask, bf16x8 &p_hi, bf16x8 &p_lo) {
     // ---- online softmax.  This lane: head r16; slot (b, k) holds key
     // b*16 + kbase + 2k.  d = x*log2(e) - m_run with the lazily moved
     // reference m_run; the tile max is only reduced when some score
     // overshoots the reference by more than the slack (always on the first
     // valid tile, where m_run = -inf).
-    const int kbase = (g & 1) * 8 + (g >> 1);
     const uint32_t vm = vmask >> kbase;
     const bool full = vmask == 0xffffffffu;  // wave-uniform
     const float c = p.scale_log2;
@@ -376,7 +364,6 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
     }
     // m_run stays -inf only while no valid key has been seen; then every
     // d is -inf and the probabilities are 0.
-    bf16x8 p_hi, p_lo;
     float psum = 0.f;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
@@ -386,7 +373,9 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
       p_lo[k] = (__bf16)(pv - (float)p_hi[k]);
     }
     l_run += psum;
-
+  };
+  // O^T += V^T . P^T over this wave's feature slice, V from the tile at st_ckv
+  auto pv = [&](const char *st_ckv, const bf16x8 &p_hi, const bf16x8 &p_lo) {
     // ---- O^T += V^T . P^T over this wave's feature slice; k-slot k of lane
     // group g is key kbase+2k (k < 4) or 16+kbase+2(k-4).
     if (FS >= 2) {
@@ -420,6 +409,58 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
         const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, p_hi, acc[fb], 0, 0, 0);
         acc[fb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, p_lo, c, 0, 0, 0);
       }
+    }
+  };
+
+  const int pre = min(n_tiles, kStages - 1);
+  for (int j = 0; j < pre; ++j) issue_tile(j);
+
+  // Waits until tile i has landed for this wave; the tiles issued after it
+  // (up to kStages - 2 of them) may stay in flight.
+  auto wait_tile = [&](int i) {
+    static_assert(kStages == 4, "the waits below assume two tiles ahead");
+    if (i + 2 < n_tiles)
+      wait_vmcnt<2 * R::kLoads>();
+    else if (i + 1 < n_tiles)
+      wait_vmcnt<R::kLoads>();
+    else
+      wait_vmcnt<0>();
+  };
+
+  if constexpr (FS >= 2) {
+    // Software pipeline: iteration i computes S^T of tile i and the PV
+    // product of tile i-1, so the PV MFMAs overlap the latency chain of the
+    // scores (LDS reads -> MFMA -> exchange).  The exchange barrier also
+    // proves every wave done with tile i-1, whose stage then receives tile
+    // i+3.  Tile i-1 stays in LDS one iteration longer, which is what the
+    // fourth stage is for; two tiles remain in flight.
+    bf16x8 p_hi = {}, p_lo = {};
+    for (int i = 0; i < n_tiles; ++i) {
+      wait_tile(i);
+      __builtin_amdgcn_s_barrier();  // every wave's share of tile i landed
+      const char *st_ckv = lds + (i % kStages) * kStageBytes;
+      f32x4 sacc[2];
+      scores(st_ckv, sacc);
+      if (i > 0) pv(lds + ((i - 1) % kStages) * kStageBytes, p_hi, p_lo);
+      xbuf[wave * 64 + lane] = sacc[0];
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): partial written, tile i-1 read
+      __builtin_amdgcn_s_barrier();
+      if (i + kStages - 1 < n_tiles) issue_tile(i + kStages - 1);
+      reduce(sacc);
+      softmax(sacc, __builtin_amdgcn_readlane(tile_masks, i), p_hi, p_lo);
+    }
+    if (n_tiles > 0) pv(lds + ((n_tiles - 1) % kStages) * kStageBytes, p_hi, p_lo);
+  } else {
+    for (int i = 0; i < n_tiles; ++i) {
+      wait_tile(i);
+      __builtin_amdgcn_s_barrier();  // every wave's share of tile i landed; tile i-1 consumed
+      if (i + kStages - 1 < n_tiles) issue_tile(i + kStages - 1);
+      const char *st_ckv = lds + (i % kStages) * kStageBytes;
+      f32x4 sacc[2];
+      scores(st_ckv, sacc);
+      bf16x8 p_hi, p_lo;
+      softmax(sacc, __builtin_amdgcn_readlane(tile_masks, i), p_hi, p_lo);
+      pv(st_ckv, p_hi, p_lo);
     }
   }
 

@@ -17,7 +17,7 @@ constexpr int kHeadDimKpe = 64;
 constexpr int kHeadsPerGroup = 16;  // MFMA N dimension: one 16-head group
 constexpr int kKeysPerTile = 32;       // keys gathered into one LDS ring stage
 constexpr int kMinTilesPerSplit = 4;   // automatic splits keep >= 4 tiles of work each
-constexpr int kMaxChunk = 2048;        // top-k entries one workgroup handles (LDS-staged ids)
+constexpr int kMaxChunk = 1024;        // top-k entries one workgroup handles (LDS-staged ids)
 
 struct AttnParams {
   const char *q_nope;  // byte strides below
@@ -36,6 +36,11 @@ struct AttnParams {
   int64_t lse_st, lse_sh;
   int32_t T, H, K, page_size;
   int64_t num_slots;
+  // slot / page_size = (slot * ps_magic) >> (31 + ps_shift) for every slot
+  // below 2^31 (round-up reciprocal: ps_shift = ceil(log2 page_size),
+  // ps_magic = floor(2^(31 + ps_shift) / page_size) + 1 < 2^32)
+  uint32_t ps_magic;
+  int32_t ps_shift;
   float scale_log2;  // sm_scale * log2(e)
   int32_t num_splits, chunk;
   float *part_acc;  // [T][S][H][512] unnormalised partial outputs

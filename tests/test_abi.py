@@ -58,8 +58,11 @@ def test_abi_version_and_struct_layout(tmp_path):
 def test_split_choice():
     lib = _lib.load()
     assert lib.dsa_attn_num_splits(64, 16, 2048, 0) == 4       # decode fills 256 CUs
-    assert lib.dsa_attn_num_splits(2048, 16, 2048, 0) == 1     # prefill needs no split
-    assert lib.dsa_attn_num_splits(256, 128, 2048, 0) == 1
+    # a workgroup stages at most 1024 slot ids, so top-2048 rows take 2 chunks
+    assert lib.dsa_attn_num_splits(2048, 16, 2048, 0) == 2
+    assert lib.dsa_attn_num_splits(256, 128, 2048, 0) == 2
+    assert lib.dsa_attn_num_splits(2048, 16, 1024, 0) == 1     # prefill needs no split
+    assert lib.dsa_attn_num_splits(8, 16, 4096, 1) == 4        # requests below the minimum are raised
     assert lib.dsa_attn_num_splits(1, 16, 2048, 0) == 16       # >= one tile per wave
     assert lib.dsa_attn_num_splits(64, 16, 2048, 16) == 16     # explicit request honoured
     assert lib.dsa_attn_num_splits(1, 16, 5, 128) == 5         # at most one key per split
@@ -67,7 +70,7 @@ def test_split_choice():
     # fp32 partial outputs, then (max, sum) pairs
     assert lib.dsa_attn_workspace_bytes(64, 16, 2048, 0) == 64 * 4 * 16 * (512 + 2) * 4
     assert lib.dsa_attn_workspace_bytes(256, 128, 2048, 2) == 256 * 2 * 128 * 514 * 4
-    assert lib.dsa_attn_workspace_bytes(2048, 16, 2048, 0) == 0
+    assert lib.dsa_attn_workspace_bytes(2048, 16, 1024, 0) == 0
 
 
 def _args(**kw):
