@@ -377,38 +377,21 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
   // O^T += V^T . P^T over this wave's feature slice, V from the tile at st_ckv
   auto pv = [&](const char *st_ckv, const bf16x8 &p_hi, const bf16x8 &p_lo) {
     // ---- O^T += V^T . P^T over this wave's feature slice; k-slot k of lane
-    // group g is key kbase+2k (k < 4) or 16+kbase+2(k-4).
-    if (FS >= 2) {
-      // Lane 16g+s points the transpose read at key row kbase + 2*(s/4)
-      // (+16 for slots 4..7), features f0 + 4*(s%4).
-      const char *vsrc = st_ckv + (kbase + 2 * (r16 >> 2)) * kCkvPitch +
-                         (fs * R::kNFB * 16 + 4 * (r16 & 3)) * 2;
+    // group g is key kbase+2k (k < 4) or 16+kbase+2(k-4).  Lane 16g+s points
+    // the transpose read at key row kbase + 2*(s/4) (+16 for slots 4..7),
+    // features f0 + 4*(s%4).  Scheduling barriers every four feature blocks
+    // keep the compiler from hoisting all reads of a wide slice (FS == 1:
+    // 64 of them) ahead of the MFMAs.
+    const char *vsrc = st_ckv + (kbase + 2 * (r16 >> 2)) * kCkvPitch +
+                       (fs * R::kNFB * 16 + 4 * (r16 & 3)) * 2;
 #pragma unroll
-      for (int fb = 0; fb < R::kNFB; ++fb) {
-        const bf16x4 lo4 = lds_read_tr16(vsrc + fb * 32);
-        const bf16x4 hi4 = lds_read_tr16(vsrc + 16 * kCkvPitch + fb * 32);
-        const bf16x8 av = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
-        const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, p_hi, acc[fb], 0, 0, 0);
-        acc[fb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, p_lo, c, 0, 0, 0);
-      }
-    } else {
-      // Full-slice waves (FS == 1) gather the V^T operand with 16-bit reads:
-      // with transpose reads the compiler hoists all 64 of them and the
-      // 8-wave variant runs out of registers.
-      const char *vcol = st_ckv + (fs * R::kNFB * 16 + r16) * 2;
-      const char *vrow[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k)
-        vrow[k] = vcol + ((k < 4) ? (kbase + 2 * k) : (16 + kbase + 2 * (k - 4))) * kCkvPitch;
-#pragma unroll
-      for (int fb = 0; fb < R::kNFB; ++fb) {
-        u16x8 a;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) a[k] = *(const unsigned short *)(vrow[k] + fb * 32);
-        const bf16x8 av = __builtin_bit_cast(bf16x8, a);
-        const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, p_hi, acc[fb], 0, 0, 0);
-        acc[fb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, p_lo, c, 0, 0, 0);
-      }
+    for (int fb = 0; fb < R::kNFB; ++fb) {
+      const bf16x4 lo4 = lds_read_tr16(vsrc + fb * 32);
+      const bf16x4 hi4 = lds_read_tr16(vsrc + 16 * kCkvPitch + fb * 32);
+      const bf16x8 av = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+      const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, p_hi, acc[fb], 0, 0, 0);
+      acc[fb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, p_lo, c, 0, 0, 0);
+      if (R::kNFB > 8 && fb % 4 == 3) __builtin_amdgcn_sched_barrier(0);
     }
   };
 
@@ -427,42 +410,29 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
       wait_vmcnt<0>();
   };
 
-  if constexpr (FS >= 2) {
-    // Software pipeline: iteration i computes S^T of tile i and the PV
-    // product of tile i-1, so the PV MFMAs overlap the latency chain of the
-    // scores (LDS reads -> MFMA -> exchange).  The exchange barrier also
-    // proves every wave done with tile i-1, whose stage then receives tile
-    // i+3.  Tile i-1 stays in LDS one iteration longer, which is what the
-    // fourth stage is for; two tiles remain in flight.
-    bf16x8 p_hi = {}, p_lo = {};
-    for (int i = 0; i < n_tiles; ++i) {
-      wait_tile(i);
-      __builtin_amdgcn_s_barrier();  // every wave's share of tile i landed
-      const char *st_ckv = lds + (i % kStages) * kStageBytes;
-      f32x4 sacc[2];
-      scores(st_ckv, sacc);
-      if (i > 0) pv(lds + ((i - 1) % kStages) * kStageBytes, p_hi, p_lo);
-      xbuf[wave * 64 + lane] = sacc[0];
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): partial written, tile i-1 read
-      __builtin_amdgcn_s_barrier();
-      if (i + kStages - 1 < n_tiles) issue_tile(i + kStages - 1);
-      reduce(sacc);
-      softmax(sacc, __builtin_amdgcn_readlane(tile_masks, i), p_hi, p_lo);
-    }
-    if (n_tiles > 0) pv(lds + ((n_tiles - 1) % kStages) * kStageBytes, p_hi, p_lo);
-  } else {
-    for (int i = 0; i < n_tiles; ++i) {
-      wait_tile(i);
-      __builtin_amdgcn_s_barrier();  // every wave's share of tile i landed; tile i-1 consumed
-      if (i + kStages - 1 < n_tiles) issue_tile(i + kStages - 1);
-      const char *st_ckv = lds + (i % kStages) * kStageBytes;
-      f32x4 sacc[2];
-      scores(st_ckv, sacc);
-      bf16x8 p_hi, p_lo;
-      softmax(sacc, __builtin_amdgcn_readlane(tile_masks, i), p_hi, p_lo);
-      pv(st_ckv, p_hi, p_lo);
-    }
+  // Software pipeline: iteration i computes S^T of tile i and the PV
+  // product of tile i-1, so the PV MFMAs overlap the latency chain of the
+  // scores (LDS reads -> MFMA -> exchange).  The second barrier (the partial
+  // exchange when FS > 1) also proves every wave done with tile i-1, whose
+  // stage then receives tile i+3.  Tile i-1 stays in LDS one iteration
+  // longer, which is what the fourth stage is for; two tiles remain in
+  // flight.
+  bf16x8 p_hi = {}, p_lo = {};
+  for (int i = 0; i < n_tiles; ++i) {
+    wait_tile(i);
+    __builtin_amdgcn_s_barrier();  // every wave's share of tile i landed
+    const char *st_ckv = lds + (i % kStages) * kStageBytes;
+    f32x4 sacc[2];
+    scores(st_ckv, sacc);
+    if (i > 0) pv(lds + ((i - 1) % kStages) * kStageBytes, p_hi, p_lo);
+    if (FS >= 2) xbuf[wave * 64 + lane] = sacc[0];
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): partial written, tile i-1 read
+    __builtin_amdgcn_s_barrier();
+    if (i + kStages - 1 < n_tiles) issue_tile(i + kStages - 1);
+    if (FS >= 2) reduce(sacc);
+    softmax(sacc, __builtin_amdgcn_readlane(tile_masks, i), p_hi, p_lo);
   }
+  if (n_tiles > 0) pv(lds + ((n_tiles - 1) % kStages) * kStageBytes, p_hi, p_lo);
 
   // ---- epilogue: lanes of a head hold partial sums over disjoint keys
   l_run += __shfl_xor(l_run, 16);
