@@ -60,7 +60,8 @@ extern "C" {
  * 64 and H a multiple of 16.  num_splits: 0 = automatic (fills the GPU),
  * otherwise the number of top-k chunks computed in parallel per token and
  * merged with log-sum-exp weights in a fixed order (results are
- * deterministic).  A split call needs dsa_attn_workspace_bytes() of workspace
+ * deterministic).  A chunk holds at most 1024 entries, so rows longer than
+ * that always run split (the count is raised to ceil(topk / 1024)).  A split call needs dsa_attn_workspace_bytes() of workspace
  * (16-byte aligned, contents irrelevant) for the fp32 partials; calls that run
  * concurrently must not share a workspace.
  */
@@ -145,10 +146,13 @@ int dsa_attn_merge(const dsa_attn_merge_args *args, void *stream);
  *
  *   score[t,s] = sum_h w[t,h] * relu(q[t,h,:] . k[s,:] * k_scale[s])
  *
- * with the exact rounding order: d = exact dot of the e4m3 codes;
- * a = fl32(fl32(d) * k_scale[s]); r = max(a, 0); v = fl32(w[t,h] * r); the
- * head sum adds blocks of 16 heads in order, each block as
- * (G0 + G1) + (G2 + G3), G = ((v0 + v1) + v2) + v3 over 4 consecutive heads.
+ * computed in the factored form k_scale[s] * sum_h w[t,h] * relu(dot), which
+ * is equal for the positive scales quantisation produces, with one exact
+ * rounding order: D_h = 2^18 * (exact dot of the e4m3fn values; NaN codes count
+ * as 0); r_h = fl32(max(D_h, 0)); the heads form 4 groups of num_heads/4
+ * consecutive heads and group g sums G_g = fma(w[t,h], r_h, G_g) in ascending
+ * head order from 0; total = fl32(fl32(G_0 + G_1) + fl32(G_2 + G_3));
+ * score = fl32(total * fl32(k_scale[s] * 2^-18)).
  * Position s is a candidate for row t iff s <= causal_limit[t].  The k
  * largest candidates are selected, ties to the lower position; rows with
  * fewer candidates are padded with -1.  Output order is ascending position.
@@ -156,10 +160,12 @@ int dsa_attn_merge(const dsa_attn_merge_args *args, void *stream);
  * block_table[t*block_table_stride + s/page_size]*page_size + s%page_size.
  *
  *   q_idx [T,num_heads,head_dim] e4m3fn codes, k_idx [S,head_dim] e4m3fn
- *   codes, k_scale [S] fp32, weights [T,num_heads] fp32, causal_limit [T]
- *   int32, out [T,topk] int32; scores_out [T,S] fp32 optional (NULL = skip;
- *   masked entries hold -inf).
- * head_dim must be 128, num_heads a multiple of 16, topk <= 4096.
+ *   codes (both 16-byte aligned), k_scale [S] fp32, weights [T,num_heads]
+ *   fp32, causal_limit [T] int32, out [T,topk] int32; scores_out [T,S] fp32
+ *   optional (NULL = not returned; masked entries hold -inf).
+ * head_dim must be 128, num_heads 16, 32, 48 or 64, topk <= 2^24.  The
+ * workspace (dsa_indexer_workspace_bytes, 256-byte aligned) holds the MFMA
+ * operand pieces of q and k and, unless scores_out is given, the scores.
  */
 typedef struct dsa_indexer_args {
   const uint8_t *q_idx;
