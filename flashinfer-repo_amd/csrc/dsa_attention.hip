@@ -208,6 +208,8 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
   const int qb0 = FS >= 2 ? (fs & 1) : 0;
   const int part = FS >= 2 ? (fs >> 1) : 0;
 
+  // the 8-slice layout shares the softmax work through LDS (softmax_shared)
+  constexpr bool kShared = W == 8 && FS == 8;
   const int k_begin = split * p.chunk;
   const int n_keys = max(0, min(p.K, k_begin + p.chunk) - k_begin);
   const int n_tiles = (n_keys + kKeysPerTile - 1) / kKeysPerTile;
@@ -374,6 +376,83 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
     }
     l_run += psum;
   };
+  // Probability exchange of the 8-slice layout (FS == 8, one head group):
+  // value v = b*4 + k of every lane (head r16, key b*16 + kbase + 2k) is
+  // computed by wave v alone and passed on through LDS, instead of every wave
+  // reducing the partial scores and exponentiating all 512 values.  The words
+  // live in the 128-byte padding after each kpe row group of the four stages,
+  // which neither the gather nor the score reads touch: value v, lane l at
+  // padding chunk 2v + l/32, word l%32.  A word is bf16 hi << 16 | bf16 lo; hi
+  // is never negative, so its sign bit carries "this value overshoots the
+  // reference max", and since every wave reads all 512 words they all take
+  // the same (rare) rescale branch.
+  auto pword = [&](int v, int l) -> uint32_t * {
+    const int c = 2 * v + (l >> 5);
+    return (uint32_t *)(lds + (c >> 2) * kStageBytes + kCkvStageBytes + (c & 3) * kKpeGroupPitch +
+                        1024 + (l & 31) * 4);
+  };
+  auto softmax_shared = [&](uint32_t vmask, bf16x8 &p_hi, bf16x8 &p_lo) {
+    const int v = wave, b = v >> 2, k = v & 3;
+    const float c = p.scale_log2;
+    // this lane's score of value v: the partials added in the order reduce() uses
+    const float *x = (const float *)xbuf;
+    float sc = x[(b * 64 + lane) * 4 + k];
+#pragma unroll
+    for (int pp = 1; pp < R::kParts; ++pp) sc += x[((b + 2 * pp) * 64 + lane) * 4 + k];
+    const bool valid = ((vmask >> (b * 16 + kbase + 2 * k)) & 1u) != 0;
+    auto publish = [&](float d, bool flag) {
+      const float pv = fast_exp2(d);
+      const __bf16 hi = (__bf16)pv;
+      const __bf16 lo = (__bf16)(pv - (float)hi);
+      const uint32_t w = ((uint32_t)__builtin_bit_cast(uint16_t, hi) | (flag ? 0x8000u : 0u)) << 16 |
+                         (uint32_t)__builtin_bit_cast(uint16_t, lo);
+      *pword(v, lane) = w;
+      return pv;
+    };
+    float d = valid ? __builtin_fmaf(sc, c, -m_run) : -INFINITY;
+    float pv = publish(d, d > kRescaleSlack);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    uint32_t w[8];
+    uint32_t flags = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      w[j] = *pword(j, lane);
+      flags |= w[j];
+    }
+    if (__ballot((flags >> 31) != 0) != 0) {  // uniform: every wave read the same 512 words
+      __builtin_amdgcn_s_barrier();           // all flags read before any word is rewritten
+      f32x4 sacc[2];
+      reduce(sacc);
+      const uint32_t vm = vmask >> kbase;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+          if ((vm >> (bb * 16 + 2 * kk)) & 1u) mx = fmaxf(mx, sacc[bb][kk] * c);
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int fb = 0; fb < R::kNFB; ++fb) acc[fb] *= alpha;
+      d = valid ? __builtin_fmaf(sc, c, -m_run) : -INFINITY;
+      pv = publish(d, false);
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      __builtin_amdgcn_s_barrier();
+#pragma unroll
+      for (int j = 0; j < 8; ++j) w[j] = *pword(j, lane);
+    }
+    l_run += pv;  // this wave's share; the shares are added at the end
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      p_hi[j] = __builtin_bit_cast(__bf16, (uint16_t)((w[j] >> 16) & 0x7fffu));
+      p_lo[j] = __builtin_bit_cast(__bf16, (uint16_t)(w[j] & 0xffffu));
+    }
+  };
   // O^T += V^T . P^T over this wave's feature slice, V from the tile at st_ckv
   auto pv = [&](const char *st_ckv, const bf16x8 &p_hi, const bf16x8 &p_lo) {
     // ---- O^T += V^T . P^T over this wave's feature slice; k-slot k of lane
@@ -429,14 +508,29 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): partial written, tile i-1 read
     __builtin_amdgcn_s_barrier();
     if (i + kStages - 1 < n_tiles) issue_tile(i + kStages - 1);
-    if (FS >= 2) reduce(sacc);
-    softmax(sacc, __builtin_amdgcn_readlane(tile_masks, i), p_hi, p_lo);
+    if constexpr (kShared) {
+      softmax_shared(__builtin_amdgcn_readlane(tile_masks, i), p_hi, p_lo);
+    } else {
+      if (FS >= 2) reduce(sacc);
+      softmax(sacc, __builtin_amdgcn_readlane(tile_masks, i), p_hi, p_lo);
+    }
   }
   if (n_tiles > 0) pv(lds + ((n_tiles - 1) % kStages) * kStageBytes, p_hi, p_lo);
 
-  // ---- epilogue: lanes of a head hold partial sums over disjoint keys
+  // ---- epilogue: lanes of a head hold partial sums over disjoint keys (and,
+  // with the probability exchange, each wave over its share of the values)
   l_run += __shfl_xor(l_run, 16);
   l_run += __shfl_xor(l_run, 32);
+  if constexpr (kShared) {
+    __builtin_amdgcn_s_barrier();  // every wave done with the exchange words
+    if (lane < 16) *pword(wave >> 1, (wave & 1) * 32 + lane) = __float_as_uint(l_run);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    float l = 0.f;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) l += __uint_as_float(*pword(w >> 1, (w & 1) * 32 + r16));
+    l_run = l;
+  }
   if (p.num_splits == 1 && !p.partial_only) {
     const float inv = (m_run == -INFINITY) ? 0.f : 1.f / l_run;
 #pragma unroll
