@@ -564,22 +564,48 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
 // kernel.py:437-493, with its -inf guards :475-476).  One workgroup per
 // (token, head); 128 threads x 4 features.  Split order is fixed, so the
 // result is deterministic.
+// SMAX > 0: at most SMAX splits, all partial loads issued before any use (one
+// memory round trip); SMAX == 0: any number of splits, loaded as consumed.
+template <int SMAX>
 __global__ __launch_bounds__(128) void dsa_attn_combine_kernel(AttnParams p) {
   const int t = blockIdx.x;
   const int head = blockIdx.y;
   const int S = p.num_splits;
   const int f0 = threadIdx.x * 4;
   const int64_t row0 = (int64_t)t * S * p.H + head;
-  float M = -INFINITY;
-  for (int s = 0; s < S; ++s) M = fmaxf(M, p.part_ml[(row0 + (int64_t)s * p.H) * 2]);
-  float L = 0.f;
+  float M = -INFINITY, L = 0.f;
   f32x4 o = {0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < S; ++s) {
-    const int64_t row = row0 + (int64_t)s * p.H;
-    const float ms = p.part_ml[row * 2];
-    const float a = (ms == -INFINITY) ? 0.f : fast_exp2(ms - M);
-    L += a * p.part_ml[row * 2 + 1];
-    o += a * *(const f32x4 *)(p.part_acc + row * kHeadDimCkv + f0);
+  if constexpr (SMAX > 0) {
+    float2 ml[SMAX];
+    f32x4 pa[SMAX];
+#pragma unroll
+    for (int s = 0; s < SMAX; ++s) {
+      if (s < S) {
+        const int64_t row = row0 + (int64_t)s * p.H;
+        ml[s] = *(const float2 *)(p.part_ml + row * 2);
+        pa[s] = *(const f32x4 *)(p.part_acc + row * kHeadDimCkv + f0);
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < SMAX; ++s)
+      if (s < S) M = fmaxf(M, ml[s].x);
+#pragma unroll
+    for (int s = 0; s < SMAX; ++s) {
+      if (s < S) {
+        const float a = (ml[s].x == -INFINITY) ? 0.f : fast_exp2(ml[s].x - M);
+        L += a * ml[s].y;
+        o += a * pa[s];
+      }
+    }
+  } else {
+    for (int s = 0; s < S; ++s) M = fmaxf(M, p.part_ml[(row0 + (int64_t)s * p.H) * 2]);
+    for (int s = 0; s < S; ++s) {
+      const int64_t row = row0 + (int64_t)s * p.H;
+      const float ms = p.part_ml[row * 2];
+      const float a = (ms == -INFINITY) ? 0.f : fast_exp2(ms - M);
+      L += a * p.part_ml[row * 2 + 1];
+      o += a * *(const f32x4 *)(p.part_acc + row * kHeadDimCkv + f0);
+    }
   }
   const float inv = (M == -INFINITY) ? 0.f : 1.f / L;
   bf16x4 ob;
@@ -619,7 +645,11 @@ hipError_t launch_attention_partial(const AttnParams &p, hipStream_t stream) {
 
 hipError_t launch_attention_merge(const AttnParams &p, hipStream_t stream) {
   if (p.T == 0) return hipSuccess;
-  hipLaunchKernelGGL(dsa_attn_combine_kernel, dim3(p.T, p.H), dim3(128), 0, stream, p);
+  const dim3 grid(p.T, p.H), block(128);
+  if (p.num_splits <= 4) hipLaunchKernelGGL(dsa_attn_combine_kernel<4>, grid, block, 0, stream, p);
+  else if (p.num_splits <= 8) hipLaunchKernelGGL(dsa_attn_combine_kernel<8>, grid, block, 0, stream, p);
+  else if (p.num_splits <= 16) hipLaunchKernelGGL(dsa_attn_combine_kernel<16>, grid, block, 0, stream, p);
+  else hipLaunchKernelGGL(dsa_attn_combine_kernel<0>, grid, block, 0, stream, p);
   return hipGetLastError();
 }
 
