@@ -169,6 +169,39 @@ def test_duplicate_slots_and_page_size_views():
     assert torch.equal(lse_a, lse_b) and torch.equal(lse_a, lse_c)
 
 
+def test_page_sizes_not_powers_of_two_and_padded_pages():
+    """Slot -> (page, offset) uses a multiply by a reciprocal of the page
+    size; every page size and a page stride larger than page_size rows must
+    give the same result as the flat view."""
+    g = torch.Generator().manual_seed(21)
+    slots = 960
+    qn = (torch.randn(3, 16, 512, generator=g)).to(torch.bfloat16)
+    qp = (torch.randn(3, 16, 64, generator=g)).to(torch.bfloat16)
+    ckv = (torch.randn(slots, 512, generator=g) * 0.7).to(torch.bfloat16)
+    kpe = (torch.randn(slots, 64, generator=g) * 0.7).to(torch.bfloat16)
+    idx = torch.stack([torch.randperm(slots, generator=g)[:700] for _ in range(3)]).to(torch.int32)
+    idx[1, 650:] = -1
+    base = dict(q_nope=qn, q_pe=qp, ckv_cache=ckv.reshape(slots, 1, 512),
+                kpe_cache=kpe.reshape(slots, 1, 64), sparse_indices=idx, sm_scale=0.07)
+    out_ref, lse_ref = _run(kernel, base)
+    _assert_parity(out_ref, lse_ref, *_oracle(base), "page size 1")
+    for ps in (3, 5, 48, 96, 320, 960):
+        d = dict(base, ckv_cache=ckv.reshape(slots // ps, ps, 512), kpe_cache=kpe.reshape(slots // ps, ps, 64))
+        out, lse = _run(kernel, d)
+        assert torch.equal(out, out_ref) and torch.equal(lse, lse_ref), f"page size {ps}"
+    # pages of 48 rows stored 50 rows apart (a page stride that is not 48 rows)
+    ck = torch.zeros(slots // 48, 50, 512, dtype=torch.bfloat16)
+    kp = torch.zeros(slots // 48, 50, 64, dtype=torch.bfloat16)
+    ck[:, :48] = ckv.reshape(slots // 48, 48, 512)
+    kp[:, :48] = kpe.reshape(slots // 48, 48, 64)
+    gc, gk = ck.to(DEV), kp.to(DEV)
+    out = torch.empty(3, 16, 512, dtype=torch.bfloat16, device=DEV)
+    lse = torch.empty(3, 16, dtype=torch.float32, device=DEV)
+    kernel_out(qn.to(DEV), qp.to(DEV), gc[:, :48], gk[:, :48], idx.to(DEV), 0.07, out, lse)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), out_ref) and torch.equal(lse.cpu(), lse_ref), "padded pages"
+
+
 def test_strided_inputs_and_dps_output():
     d = workloads.cfg2(T=5, seed=11)
     g = workloads.to_device(d, DEV)
