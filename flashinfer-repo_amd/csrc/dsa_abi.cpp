@@ -72,15 +72,18 @@ void choose_splits(int64_t T, int64_t H, int64_t K, int32_t requested, int32_t *
   *chunk = (int32_t)c;
 }
 
-// Workspace of a split call: [partial outputs T x S x H x 512 fp32]
+// Partials of dsa_attn_fwd_partial: [partial outputs T x S x H x 512 fp32]
 // [(max, sum) T x S x H fp32].
 size_t partial_bytes(int64_t T, int64_t H, int32_t S) {
   const size_t rows = (size_t)T * (size_t)S * (size_t)H;
   return rows * dsa::kHeadDimCkv * sizeof(float) + rows * 2 * sizeof(float);
 }
 
+// Workspace of a split dsa_attn_fwd: the same partial outputs, then room for
+// the in-kernel merge's (max, sum) copies, one per feature slice (T x S x H x 8).
 size_t attn_workspace(int64_t T, int64_t H, int32_t S) {
-  return S <= 1 ? 0 : partial_bytes(T, H, S);
+  const size_t rows = (size_t)T * (size_t)S * (size_t)H;
+  return S <= 1 ? 0 : rows * dsa::kHeadDimCkv * sizeof(float) + rows * 16 * sizeof(float);
 }
 
 }  // namespace
@@ -103,6 +106,14 @@ size_t dsa_attn_workspace_bytes(int64_t num_tokens, int64_t num_heads, int64_t t
   int32_t s, c;
   choose_splits(num_tokens, num_heads, topk, requested_splits, &s, &c);
   return attn_workspace(num_tokens, num_heads, s);
+}
+
+size_t dsa_attn_counter_bytes(int64_t num_tokens, int64_t num_heads) {
+  if (num_tokens <= 0 || num_heads < dsa::kHeadsPerGroup || num_heads > 4096 ||
+      !dsa::attn_merges_in_kernel((int)num_heads))
+    return 0;
+  return (size_t)dsa::attn_counter_words(num_tokens, dsa::attn_head_blocks((int)num_heads)) *
+         sizeof(uint32_t);
 }
 
 }  // extern "C"
@@ -158,6 +169,16 @@ int prepare_attn(const char *fn, const dsa_attn_args *a, bool partial_only, dsa:
   if (need > 0 && (!a->workspace || a->workspace_bytes < need || !aligned(a->workspace, 16)))
     return fail(DSA_EWORKSPACE, "%s: workspace of %zu bytes (16-byte aligned) needed, got %zu",
                 fn, need, a->workspace ? a->workspace_bytes : (size_t)0);
+  const bool merge_in_kernel = !partial_only && S > 1 && a->split_counters != nullptr &&
+                               dsa::attn_merges_in_kernel((int)a->num_heads);
+  if (merge_in_kernel) {
+    const size_t cneed = (size_t)dsa::attn_counter_words(
+                             a->num_tokens, dsa::attn_head_blocks((int)a->num_heads)) *
+                         sizeof(uint32_t);
+    if (a->split_counters_bytes < cneed || !aligned(a->split_counters, 4))
+      return fail(DSA_EWORKSPACE, "%s: split_counters of %zu bytes (4-byte aligned) needed, got %zu",
+                  fn, cneed, a->split_counters_bytes);
+  }
 
   p->q_nope = static_cast<const char *>(a->q_nope);
   p->qn_st = a->q_nope_stride_t * 2;
@@ -197,6 +218,7 @@ int prepare_attn(const char *fn, const dsa_attn_args *a, bool partial_only, dsa:
   p->part_acc = ws;
   p->part_ml = ws ? ws + (size_t)a->num_tokens * S * a->num_heads * dsa::kHeadDimCkv : nullptr;
   p->partial_only = partial_only ? 1 : 0;
+  p->counters = merge_in_kernel ? a->split_counters : nullptr;
   return DSA_OK;
 }
 

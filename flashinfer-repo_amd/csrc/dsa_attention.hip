@@ -74,6 +74,13 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+// Raw buffer resources (stride 0, byte-sized range, 32-bit data format) and
+// the sc1 cache policy bit of buffer loads and stores (device coherence).
+constexpr int kBufferFlags = 0x00020000;
+constexpr int kSC1 = 16;
 
 // LDS geometry (bytes).  A ckv row is padded from 1024 to 1040 B so the 16
 // rows one MFMA operand read touches fall in distinct banks; kpe rows are
@@ -547,16 +554,139 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
     return;
   }
 
-  // ---- split: write this chunk's partial for dsa_attn_combine_kernel
-  const int64_t prow = ((int64_t)t * p.num_splits + split) * p.H + head;
+  // ---- split: write this chunk's partial
+  const int S = p.num_splits;
+  const int64_t prow = ((int64_t)t * S + split) * p.H + head;
+  // (The in-kernel merge is built for the 8-slice layout only: with fewer
+  // slices a wave owns more feature blocks, its merge takes one memory round
+  // trip per 4 of them, and the tail costs more than the merge kernel.)
+  if (FS != 8 || p.counters == nullptr) {  // dsa_attn_combine_kernel merges
 #pragma unroll
-  for (int fb = 0; fb < R::kNFB; ++fb) {
-    const int f0 = (fs * R::kNFB + fb) * 16 + 4 * g;
-    *(f32x4 *)(p.part_acc + prow * kHeadDimCkv + f0) = acc[fb];
+    for (int fb = 0; fb < R::kNFB; ++fb) {
+      const int f0 = (fs * R::kNFB + fb) * 16 + 4 * g;
+      *(f32x4 *)(p.part_acc + prow * kHeadDimCkv + f0) = acc[fb];
+    }
+    if (fs == 0 && lane < 16) {
+      p.part_ml[prow * 2 + 0] = m_run;
+      p.part_ml[prow * 2 + 1] = l_run;
+    }
+    return;
   }
-  if (fs == 0 && lane < 16) {
-    p.part_ml[prow * 2 + 0] = m_run;
-    p.part_ml[prow * 2 + 1] = l_run;
+
+  if constexpr (FS == 8) {
+  // ---- in-kernel merge.  A wave's feature slice of its head group depends
+  // only on the same slice of the other chunks, so each wave counts arrivals
+  // on its own counter (no workgroup-wide flag, no barrier) and exchanges its
+  // partial through a private region in lane order (kNFB x 1 KB of acc, then
+  // 16 (m, l) pairs), one contiguous 1 KB per store instruction.  The chunks
+  // of a token run on different XCDs, whose L2s are not coherent with each
+  // other.  A device-scope release/acquire fence pair would write back /
+  // invalidate the whole L2 (buffer_wbl2 / buffer_inv), which costs more than
+  // the second launch it saves; instead the exchange uses sc1 accesses
+  // (device-coherent: written through to, and read from, the memory side, as
+  // device-scope atomics are) and the wave waits for its stores to complete
+  // (vmcnt(0); stores count there) before it draws a ticket.  The wave that
+  // draws the last ticket resets the counter for the next launch and merges
+  // the slice in split order with the merge kernel's arithmetic, so both
+  // paths give the same bits whichever chunk finishes last.
+  // Regions of workgroup (t, s, blockIdx.y): its W waves' acc regions tile
+  // exactly the workgroup's share of part_acc (kHG x 16 heads x 512 fp32),
+  // and its W x 16 (m, l) pairs fit in the share of part_ml the host sizes
+  // (kHG x 16 heads x 8 pairs).
+  static_assert(W * R::kNFB * 256 == R::kHG * kHeadsPerGroup * kHeadDimCkv, "acc regions");
+  static_assert(W * 32 <= R::kHG * kHeadsPerGroup * 16, "(m, l) regions");
+  const int64_t wg0 = (int64_t)t * S * gridDim.y + blockIdx.y;  // chunk s: + s * gridDim.y
+  auto acc_region = [&](int s) {
+    const int64_t w = ((wg0 + (int64_t)s * gridDim.y) * W + wave) * (R::kNFB * 256);
+    return __builtin_amdgcn_make_buffer_rsrc(p.part_acc + w, 0, R::kNFB * 1024, kBufferFlags);
+  };
+  auto ml_region = [&](int s) {
+    const int64_t w = ((wg0 + (int64_t)s * gridDim.y) * W + wave) * 32;
+    return __builtin_amdgcn_make_buffer_rsrc(p.part_ml + w, 0, 128, kBufferFlags);
+  };
+  {
+    const auto ar = acc_region(split);
+#pragma unroll
+    for (int fb = 0; fb < R::kNFB; ++fb)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[fb]), ar,
+                                             (fb * 64 + lane) * 16, 0, kSC1);
+    if (lane < 16)
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, make_float2(m_run, l_run)),
+                                            ml_region(split), lane * 8, 0, kSC1);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  uint32_t *cnt = p.counters + ((int64_t)t * gridDim.y + blockIdx.y) * 8 + wave;
+  uint32_t ticket = 0;
+  if (lane == 0) ticket = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  ticket = __shfl(ticket, 0);
+  if (ticket != (uint32_t)(S - 1)) return;
+  if (lane == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  auto load_ml = [&](int s) {
+    return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(ml_region(s), r16 * 8, 0, kSC1));
+  };
+  constexpr int kB = 4;                           // chunks whose loads are in flight together
+  constexpr int kF = R::kNFB < 4 ? R::kNFB : 4;   // feature blocks per load batch
+  // The max over chunks comes first; with at most kB chunks it is taken from
+  // the first load batch itself (one memory round trip fewer).
+  float M = -INFINITY;
+  for (int s0 = 0; S > kB && s0 < S; s0 += kB) {
+    float mv[kB];
+#pragma unroll
+    for (int j = 0; j < kB; ++j) mv[j] = load_ml(min(s0 + j, S - 1)).x;
+#pragma unroll
+    for (int j = 0; j < kB; ++j) M = fmaxf(M, mv[j]);  // clamped repeats leave the max alone
+  }
+  // Feature blocks in batches of kF (bounded registers in the 1-slice
+  // layouts); the sum L is complete after the first batch.
+  float L = 0.f, inv = 0.f;
+#pragma unroll
+  for (int fc = 0; fc < R::kNFB; fc += kF) {
+    f32x4 o[kF];
+#pragma unroll
+    for (int f = 0; f < kF; ++f) o[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < S; s0 += kB) {
+      float a[kB];
+      float2 ml[kB];
+      f32x4 pa[kB][kF];
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        const int s = min(s0 + j, S - 1);
+        ml[j] = load_ml(s);
+        const auto ar = acc_region(s);
+#pragma unroll
+        for (int f = 0; f < kF; ++f)
+          pa[j][f] = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(ar, ((fc + f) * 64 + lane) * 16, 0, kSC1));
+      }
+      if (S <= kB) {
+#pragma unroll
+        for (int j = 0; j < kB; ++j) M = fmaxf(M, ml[j].x);
+      }
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        a[j] = (ml[j].x == -INFINITY) ? 0.f : fast_exp2(ml[j].x - M);
+        if (fc == 0 && s0 + j < S) L += a[j] * ml[j].y;
+      }
+#pragma unroll
+      for (int j = 0; j < kB; ++j)
+        if (s0 + j < S) {
+#pragma unroll
+          for (int f = 0; f < kF; ++f) o[f] += a[j] * pa[j][f];
+        }
+    }
+    if (fc == 0) inv = (M == -INFINITY) ? 0.f : 1.f / L;
+#pragma unroll
+    for (int f = 0; f < kF; ++f) {
+      const int f0 = (fs * R::kNFB + fc + f) * 16 + 4 * g;
+      bf16x4 ob;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) ob[k] = (__bf16)(o[f][k] * inv);
+      *(bf16x4 *)(p.out + t * p.out_st + head * p.out_sh + f0 * 2) = ob;
+    }
+  }
+  if (fs == 0 && lane < 16)
+    p.lse[t * p.lse_st + head * p.lse_sh] = (M == -INFINITY) ? -INFINITY : M + __log2f(L);
   }
 }
 
@@ -625,6 +755,8 @@ hipError_t launch_ring(const AttnParams &p, int head_blocks, hipStream_t stream)
 
 }  // namespace
 
+bool attn_merges_in_kernel(int H) { return (H / kHeadsPerGroup) % 2 != 0; }  // the <8, 8> layout
+
 int attn_head_blocks(int H) {
   const int groups = H / kHeadsPerGroup;
   if (groups % 8 == 0) return groups / 8;
@@ -653,9 +785,11 @@ hipError_t launch_attention_merge(const AttnParams &p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_attention(const AttnParams &p, hipStream_t stream) {
+hipError_t launch_attention(const AttnParams &pin, hipStream_t stream) {
+  AttnParams p = pin;
+  if (!attn_merges_in_kernel(p.H)) p.counters = nullptr;
   hipError_t e = launch_attention_partial(p, stream);
-  if (e != hipSuccess || (p.num_splits == 1 && !p.partial_only)) return e;
+  if (e != hipSuccess || (p.num_splits == 1 && !p.partial_only) || p.counters != nullptr) return e;
   return launch_attention_merge(p, stream);
 }
 

@@ -43,13 +43,28 @@ struct AttnParams {
   int32_t ps_shift;
   float scale_log2;  // sm_scale * log2(e)
   int32_t num_splits, chunk;
-  float *part_acc;  // [T][S][H][512] unnormalised partial outputs
-  float *part_ml;   // [T][S][H][2]   (reference max in log2 units, sum)
+  // Unnormalised partial outputs and (reference max in log2 units, sum):
+  // for the merge kernel [T][S][H][512] and [T][S][H][2]; for the in-kernel
+  // merge the same part_acc space in per-wave lane-order regions and 16
+  // pairs per wave in part_ml (room for [T][S][H][16] floats).
+  float *part_acc;
+  float *part_ml;
   int32_t partial_only;  // write partials even when num_splits == 1
+  // Split merge inside the attention kernel: per-wave arrival counters
+  // [T][head blocks][8], zero before the launch and left zero by it.  Null:
+  // the separate merge kernel runs.
+  uint32_t *counters;
 };
+
+// Counter words a split call with in-kernel merge uses.
+inline int64_t attn_counter_words(int64_t T, int head_blocks) { return T * head_blocks * 8; }
 
 // Workgroups per token along the head axis (each covers up to 8 groups of 16).
 int attn_head_blocks(int H);
+// Whether split calls with counters merge inside the attention kernel for H
+// heads (the layout with 8 feature slices per head group); otherwise the
+// merge kernel runs and the counters are not touched.
+bool attn_merges_in_kernel(int H);
 
 // Whole call: per-chunk attention, then (num_splits > 1) the merge.
 hipError_t launch_attention(const AttnParams &p, hipStream_t stream);

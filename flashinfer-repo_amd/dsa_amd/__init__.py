@@ -11,8 +11,8 @@ Hand-written HIP kernels behind a C ABI (``include/dsa_abi.h``,
 """
 from .indexer_kernel import run_indexer_and_topk, run_sparse_attention_pipeline  # noqa: F401
 from .kernel import (kernel, kernel_out, kernel_partial, kernel_splitk, kernel_splitk_v2,  # noqa: F401
-                     merge_partials, new_workspace, num_splits)
+                     merge_partials, new_split_counters, new_workspace, num_splits)
 
 __all__ = ["kernel", "kernel_splitk", "kernel_splitk_v2", "kernel_out", "kernel_partial",
-           "merge_partials", "new_workspace", "num_splits", "run_indexer_and_topk",
+           "merge_partials", "new_split_counters", "new_workspace", "num_splits", "run_indexer_and_topk",
            "run_sparse_attention_pipeline"]

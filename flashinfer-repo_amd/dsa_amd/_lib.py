@@ -16,7 +16,7 @@ DSA_EINVAL = 1
 DSA_EUNSUPPORTED = 2
 DSA_ELAUNCH = 3
 DSA_EWORKSPACE = 4
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 EXPORTED_SYMBOLS = (
     "dsa_attn_fwd",
@@ -25,6 +25,7 @@ EXPORTED_SYMBOLS = (
     "dsa_attn_num_splits",
     "dsa_attn_partial_bytes",
     "dsa_attn_workspace_bytes",
+    "dsa_attn_counter_bytes",
     "dsa_indexer_topk",
     "dsa_indexer_workspace_bytes",
     "dsa_last_error",
@@ -52,6 +53,7 @@ class AttnArgs(ctypes.Structure):
         ("sm_scale", ctypes.c_float),
         ("num_splits", ctypes.c_int32),
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+        ("split_counters", _vp), ("split_counters_bytes", ctypes.c_size_t),
     ]
 
 
@@ -117,6 +119,8 @@ def load() -> ctypes.CDLL:
     lib.dsa_attn_num_splits.restype = ctypes.c_int32
     lib.dsa_attn_workspace_bytes.argtypes = [_i64, _i64, _i64, ctypes.c_int32]
     lib.dsa_attn_workspace_bytes.restype = ctypes.c_size_t
+    lib.dsa_attn_counter_bytes.argtypes = [_i64, _i64]
+    lib.dsa_attn_counter_bytes.restype = ctypes.c_size_t
     lib.dsa_indexer_topk.argtypes = [ctypes.POINTER(IndexerArgs), _vp]
     lib.dsa_indexer_topk.restype = ctypes.c_int
     lib.dsa_indexer_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64]

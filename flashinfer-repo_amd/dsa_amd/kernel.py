@@ -44,6 +44,40 @@ def new_workspace(q_nope: torch.Tensor, topk: int, num_splits: int = 0) -> torch
     return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q_nope.device)
 
 
+def new_split_counters(q_nope: torch.Tensor) -> torch.Tensor:
+    """Zeroed merge counters for calls of up to ``q_nope``'s token and head
+    counts (pass to :func:`kernel_out`).  Split calls of head counts with an
+    odd number of 16-head groups (e.g. H=16 decode) that are given them merge
+    their chunks inside the attention kernel and leave them zero again (other
+    head counts ignore them); calls that may run at the same time (other
+    streams, graphs replayed concurrently) each need their own."""
+    T, H, _ = q_nope.shape
+    nbytes = _lib.load().dsa_attn_counter_bytes(T, H)
+    return torch.zeros(max(nbytes // 4, 1), dtype=torch.int32, device=q_nope.device)
+
+
+# Merge counters of calls that bring none, one buffer per (device, stream):
+# calls on one stream run one after another and each leaves the counters zero.
+# A graph captured on a stream whose buffer an eager call has already made
+# large enough uses that buffer in every replay; otherwise (a buffer made
+# during capture would only be zeroed when the graph first replays) the
+# captured call merges with the separate merge kernel.
+_stream_counters = {}
+
+
+def _default_counters(dev: torch.device, nbytes: int) -> Optional[torch.Tensor]:
+    key = (dev.index, _stream_handle(dev))
+    buf = _stream_counters.get(key)
+    if buf is not None and buf.numel() * 4 >= nbytes:
+        return buf
+    if torch.cuda.is_current_stream_capturing():
+        return None
+    words = max(nbytes // 4, 2 * buf.numel() if buf is not None else 0, 4096)
+    buf = torch.zeros(words, dtype=torch.int32, device=dev)
+    _stream_counters[key] = buf
+    return buf
+
+
 def _inner_contiguous(x: torch.Tensor) -> torch.Tensor:
     return x if x.stride(-1) == 1 else x.contiguous()
 
@@ -112,7 +146,8 @@ def _attn_args(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, num
 
 def _attention(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, num_splits: int,
                output: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
-               workspace: Optional[torch.Tensor] = None):
+               workspace: Optional[torch.Tensor] = None,
+               split_counters: Optional[torch.Tensor] = None):
     a, keep, T, H, K, dev = _attn_args(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices,
                                        sm_scale, num_splits)
     if output is None:
@@ -140,6 +175,19 @@ def _attention(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, num
     a.lse, a.lse_stride_t, a.lse_stride_h = lse.data_ptr(), lse.stride(0), lse.stride(1)
     a.workspace = ws.data_ptr() if ws is not None else None
     a.workspace_bytes = ws_bytes
+    c_bytes = lib.dsa_attn_counter_bytes(T, H) if ws is not None else 0
+    if c_bytes:
+        if split_counters is not None:
+            _check(split_counters.device == dev and split_counters.is_contiguous()
+                   and split_counters.dtype == torch.int32
+                   and split_counters.numel() * 4 >= c_bytes,
+                   f"split_counters must be a contiguous int32 tensor of >= {c_bytes // 4} "
+                   f"elements on {dev} (see new_split_counters)")
+            cnt = split_counters
+        else:
+            cnt = _default_counters(dev, c_bytes)
+        if cnt is not None:
+            a.split_counters, a.split_counters_bytes = cnt.data_ptr(), cnt.numel() * 4
     _lib.check("dsa_attn_fwd", lib.dsa_attn_fwd(ctypes.byref(a), _stream_handle(dev)))
     del keep
     return output, lse
@@ -170,13 +218,16 @@ def kernel_splitk_v2(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scal
 
 
 def kernel_out(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, output, lse,
-               num_splits: int = 0, workspace: Optional[torch.Tensor] = None):
+               num_splits: int = 0, workspace: Optional[torch.Tensor] = None,
+               split_counters: Optional[torch.Tensor] = None):
     """Destination-passing variant: writes into ``output`` and ``lse``.
 
     ``workspace`` (optional) comes from :func:`new_workspace`; by default one
-    is taken from the framework's caching allocator for the call."""
+    is taken from the framework's caching allocator for the call.
+    ``split_counters`` (optional) comes from :func:`new_split_counters`; by
+    default the calls of one stream share a zeroed buffer kept per stream."""
     _attention(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, int(num_splits),
-               output=output, lse=lse, workspace=workspace)
+               output=output, lse=lse, workspace=workspace, split_counters=split_counters)
     return output, lse
 
 

@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define DSA_ABI_VERSION 1
+#define DSA_ABI_VERSION 2
 
 #define DSA_OK 0
 #define DSA_EINVAL 1      /* bad pointer, size, stride or alignment */
@@ -61,9 +61,21 @@ extern "C" {
  * otherwise the number of top-k chunks computed in parallel per token and
  * merged with log-sum-exp weights in a fixed order (results are
  * deterministic).  A chunk holds at most 1024 entries, so rows longer than
- * that always run split (the count is raised to ceil(topk / 1024)).  A split call needs dsa_attn_workspace_bytes() of workspace
- * (16-byte aligned, contents irrelevant) for the fp32 partials; calls that run
- * concurrently must not share a workspace.
+ * that always run split (the count is raised to ceil(topk / 1024)).  A split
+ * call needs dsa_attn_workspace_bytes() of workspace (16-byte aligned, contents
+ * irrelevant) for the fp32 partials.
+ *
+ * split_counters (optional, no counterpart in the reference): with NULL a
+ * split call runs a second kernel that merges the partials (the reference's
+ * kernel_splitk launch pair, kernel.py:534 and :555).  Where
+ * dsa_attn_counter_bytes() is not 0 (head counts of an odd number of 16-head
+ * groups, e.g. H=16 decode) and that much 4-byte aligned, all-zero memory is
+ * given, the merge happens inside the attention kernel instead (the
+ * workgroup that finishes a token's chunk last merges it; same bits as the
+ * two-kernel path) and every call that completes leaves the counters zero
+ * again, so zero them once (e.g. hipMemset) and reuse them for calls of any
+ * shape.  Otherwise the counters are ignored.  Calls that run concurrently
+ * must share neither a workspace nor counters.
  */
 typedef struct dsa_attn_args {
   const void *q_nope;
@@ -87,6 +99,8 @@ typedef struct dsa_attn_args {
   int32_t num_splits;
   void *workspace;
   size_t workspace_bytes;
+  uint32_t *split_counters;
+  size_t split_counters_bytes;
 } dsa_attn_args;
 
 int dsa_attn_fwd(const dsa_attn_args *args, void *stream);
@@ -98,6 +112,11 @@ int32_t dsa_attn_num_splits(int64_t num_tokens, int64_t num_heads, int64_t topk,
 /* Workspace dsa_attn_fwd needs (0 when one split suffices). */
 size_t dsa_attn_workspace_bytes(int64_t num_tokens, int64_t num_heads, int64_t topk,
                                 int32_t requested_splits);
+
+/* Size of dsa_attn_args.split_counters for num_tokens tokens of num_heads
+ * heads (any top-k and split count); 0 when calls with this head count always
+ * merge with the separate kernel. */
+size_t dsa_attn_counter_bytes(int64_t num_tokens, int64_t num_heads);
 
 /*
  * The two halves of a split dsa_attn_fwd, for callers that merge partials

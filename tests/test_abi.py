@@ -37,7 +37,7 @@ def test_header_functions_are_exported():
 def test_abi_version_and_struct_layout(tmp_path):
     """The ctypes mirrors match the C structs field by field (gcc offsetof)."""
     lib = _lib.load()
-    assert lib.dsa_abi_version() == 1
+    assert lib.dsa_abi_version() == _lib.ABI_VERSION == 2
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "dsa_abi.h"', 'int main(void){']
     for cname, cls in (("dsa_attn_args", _lib.AttnArgs), ("dsa_indexer_args", _lib.IndexerArgs)):
         lines.append(f'printf("{cname} %zu\\n", sizeof({cname}));')
@@ -68,9 +68,16 @@ def test_split_choice():
     assert lib.dsa_attn_num_splits(1, 16, 5, 128) == 5         # at most one key per split
     assert lib.dsa_attn_num_splits(4, 16, 0, 0) == 1
     # fp32 partial outputs, then (max, sum) pairs
-    assert lib.dsa_attn_workspace_bytes(64, 16, 2048, 0) == 64 * 4 * 16 * (512 + 2) * 4
-    assert lib.dsa_attn_workspace_bytes(256, 128, 2048, 2) == 256 * 2 * 128 * 514 * 4
+    assert lib.dsa_attn_workspace_bytes(64, 16, 2048, 0) == 64 * 4 * 16 * (512 + 16) * 4
+    assert lib.dsa_attn_workspace_bytes(256, 128, 2048, 2) == 256 * 2 * 128 * 528 * 4
     assert lib.dsa_attn_workspace_bytes(2048, 16, 1024, 0) == 0
+    # in-kernel merge (8-slice layout: odd numbers of 16-head groups): 8 wave
+    # counters per (token, workgroup along the heads); other layouts use none
+    assert lib.dsa_attn_counter_bytes(64, 16) == 64 * 8 * 4
+    assert lib.dsa_attn_counter_bytes(4, 48) == 4 * 3 * 8 * 4    # 3 groups, one workgroup each
+    assert lib.dsa_attn_counter_bytes(256, 128) == 0
+    assert lib.dsa_attn_counter_bytes(8, 32) == 0
+    assert lib.dsa_attn_counter_bytes(0, 16) == 0
 
 
 def _args(**kw):
@@ -109,6 +116,10 @@ def _call(a):
     (dict(output=0x6002), _lib.DSA_EINVAL, "8-byte"),
     (dict(), _lib.DSA_EWORKSPACE, "workspace"),            # decode needs 4 splits
     (dict(num_splits=2, workspace=0x8000, workspace_bytes=16), _lib.DSA_EWORKSPACE, "workspace"),
+    (dict(workspace=0x8000, workspace_bytes=1 << 30, split_counters=0x9000,
+          split_counters_bytes=64), _lib.DSA_EWORKSPACE, "split_counters"),
+    (dict(workspace=0x8000, workspace_bytes=1 << 30, split_counters=0x9002,
+          split_counters_bytes=1 << 20), _lib.DSA_EWORKSPACE, "split_counters"),
 ])
 def test_host_validation_rejects_before_launch(kw, code, needle):
     rc, msg = _call(_args(**kw))

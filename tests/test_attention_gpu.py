@@ -18,7 +18,7 @@ import torch
 import oracle
 from conftest import LSE_ATOL, LSE_RTOL, OUT_ATOL, OUT_RTOL, mismatches
 from dsa_amd import (kernel, kernel_out, kernel_partial, kernel_splitk, kernel_splitk_v2,
-                     merge_partials, new_workspace, workloads)
+                     merge_partials, new_split_counters, new_workspace, workloads)
 
 pytestmark = pytest.mark.gpu
 
@@ -308,3 +308,107 @@ def test_partials_merge_and_sharded_cache():
                                 torch.cat([pa[1], pe[1], pb[1]], 1))
     torch.cuda.synchronize()
     assert torch.equal(out3, out2) and torch.equal(lse3, lse2)
+
+
+def _merge_kernel_path(q_nope, q_pe, ckv, kpe, idx, scale, num_splits):
+    """dsa_attn_fwd through ctypes with split_counters = NULL: the chunks are
+    merged by the separate merge kernel."""
+    import ctypes
+    import importlib
+    from dsa_amd import _lib
+    kmod = importlib.import_module("dsa_amd.kernel")
+    a, keep, T, H, K, dev = kmod._attn_args(q_nope, q_pe, ckv, kpe, idx, scale, num_splits)
+    lib = _lib.load()
+    out = torch.empty((T, H, 512), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((T, H), dtype=torch.float32, device=dev)
+    ws = torch.empty(max(lib.dsa_attn_workspace_bytes(T, H, K, num_splits), 16), dtype=torch.uint8,
+                     device=dev)
+    a.output, a.out_stride_t, a.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
+    a.lse, a.lse_stride_t, a.lse_stride_h = lse.data_ptr(), lse.stride(0), lse.stride(1)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    a.split_counters, a.split_counters_bytes = None, 0
+    _lib.check("dsa_attn_fwd", lib.dsa_attn_fwd(ctypes.byref(a), kmod._stream_handle(dev)))
+    del keep
+    return out, lse
+
+
+def _heads(d, H, seed):
+    """cfg2-style inputs widened to H heads (fresh seeded queries)."""
+    gen = torch.Generator().manual_seed(seed)
+    T = d["q_nope"].shape[0]
+    d = dict(d)
+    d["q_nope"] = torch.randn(T, H, 512, generator=gen).to(torch.bfloat16)
+    d["q_pe"] = torch.randn(T, H, 64, generator=gen).to(torch.bfloat16)
+    return d
+
+
+@pytest.mark.parametrize("H,T,splits", [(16, 8, 0), (16, 8, 3), (16, 4, 17), (16, 3, 40),
+                                        (32, 6, 5), (48, 5, 3), (64, 4, 2), (128, 4, 2)])
+def test_in_kernel_merge_matches_merge_kernel_bitwise(H, T, splits):
+    """The merge inside the attention kernel (per-wave arrival counters) gives
+    the same bits as the separate merge kernel and as kernel_partial +
+    merge_partials, for every kernel layout, and leaves its counters zero."""
+    d = _heads(workloads.cfg2(T=T, seed=90 + H), H, seed=H * 7 + T)
+    g = workloads.to_device(d, DEV)
+    args = (g["q_nope"], g["q_pe"], g["ckv_cache"], g["kpe_cache"], g["sparse_indices"],
+            d["sm_scale"])
+    print(f"in-kernel merge H={H} T={T} splits={splits}", flush=True)
+    cnt = new_split_counters(g["q_nope"])
+    out = torch.empty((T, H, 512), dtype=torch.bfloat16, device=DEV)
+    lse = torch.empty((T, H), dtype=torch.float32, device=DEV)
+    kernel_out(*args, out, lse, num_splits=splits, split_counters=cnt)
+    ref_out, ref_lse = _merge_kernel_path(*args, splits)
+    acc, ml = kernel_partial(*args, num_splits=splits)
+    p_out, p_lse = merge_partials(acc, ml)
+    torch.cuda.synchronize()
+    assert int((cnt != 0).sum()) == 0, "counters not reset"
+    assert torch.equal(out, ref_out) and torch.equal(lse, ref_lse)
+    assert torch.equal(out, p_out) and torch.equal(lse, p_lse)
+    if H == 16 and splits in (0, 17):
+        _assert_parity(out.cpu(), lse.cpu(), *_oracle(d), f"in-kernel merge splits={splits}")
+
+
+def test_in_kernel_merge_counters_reused_across_calls_and_shapes():
+    """One counter buffer serves consecutive calls of different shapes and
+    split counts; each result equals the merge-kernel path."""
+    big = workloads.to_device(workloads.cfg2(T=16, seed=301), DEV)
+    cnt = new_split_counters(big["q_nope"])
+    cases = [(16, 16, 301, 0), (3, 48, 302, 5), (16, 16, 303, 4), (1, 16, 304, 0), (9, 32, 305, 7)]
+    for T, H, seed, splits in cases:
+        d = _heads(workloads.cfg2(T=T, seed=seed), H, seed=seed)
+        g = workloads.to_device(d, DEV)
+        args = (g["q_nope"], g["q_pe"], g["ckv_cache"], g["kpe_cache"], g["sparse_indices"],
+                d["sm_scale"])
+        out = torch.empty((T, H, 512), dtype=torch.bfloat16, device=DEV)
+        lse = torch.empty((T, H), dtype=torch.float32, device=DEV)
+        kernel_out(*args, out, lse, num_splits=splits, split_counters=cnt)
+        ref_out, ref_lse = _merge_kernel_path(*args, splits)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref_out) and torch.equal(lse, ref_lse), (T, H, splits)
+        assert int((cnt != 0).sum()) == 0
+
+
+def test_in_kernel_merge_graph_replays():
+    """A graph captured on a stream whose counters an eager call already made
+    merges in-kernel; every replay (new queries copied in between, eager work
+    and synchronisation between replays) equals the merge-kernel path."""
+    d = workloads.cfg2(T=24, seed=311)
+    g = workloads.to_device(d, DEV)
+    args = (g["q_nope"], g["q_pe"], g["ckv_cache"], g["kpe_cache"], g["sparse_indices"],
+            d["sm_scale"])
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        kernel(*args)                      # makes the capture stream's counters
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        gout, glse = kernel(*args)
+    gen = torch.Generator().manual_seed(312)
+    for i in range(4):
+        g["q_nope"].copy_(torch.randn(g["q_nope"].shape, generator=gen).to(torch.bfloat16))
+        graph.replay()
+        ref_out, ref_lse = _merge_kernel_path(*args, 0)
+        torch.cuda.synchronize()
+        assert torch.equal(gout, ref_out) and torch.equal(glse, ref_lse), f"replay {i}"
