@@ -39,12 +39,13 @@
 //
 // Splits.  With one chunk per token the workgroup writes the bf16 output and
 // lse directly.  Otherwise each workgroup writes an unnormalised fp32 partial
-// (acc, m, l) and dsa_attn_combine_kernel merges a token's partials with
-// log-sum-exp weights in split order (reference merge algebra:
-// kernel.py:461-493, -inf guards :475-476), so results are deterministic.
-// (Merging inside the gather kernel, last-arriving workgroup style, needs a
-// device-scope release per workgroup -- an L2 write-back on this part -- and
-// measured slower than the second launch.)
+// (acc, m, l) and the partials of a token are merged with log-sum-exp
+// weights in split order (reference merge algebra: kernel.py:461-493, -inf
+// guards :475-476), so results are deterministic: in the 8-slice layout
+// inside this kernel by the wave that finishes a feature slice last (device-
+// coherent sc1 stores and loads plus a per-wave arrival counter, no L2
+// write-back), otherwise by dsa_attn_combine_kernel.  Both give the same
+// bits.
 //
 // MFMA 16x16x32 bf16 lane layout used throughout (lane = 16*g + r):
 //   A (16 x 32): lane holds row r, k-slots 8g..8g+7
