@@ -316,14 +316,36 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
       sacc[bb] = qk_part<R::kParts>(part, rowp, kp, qreg, g);
     }
   };
+  // Partial S^T exchange: slot w holds wave w's partial of its key block.
+  // The 8-slice layout reads single components (softmax_shared), so it keeps
+  // them component-major (each read is 64 consecutive words, no bank
+  // conflicts); the others read whole f32x4 per lane.
+  auto xput = [&](const f32x4 &v) {
+    if constexpr (kShared) {
+      float *x = (float *)xbuf;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) x[(wave * 4 + k) * 64 + lane] = v[k];
+    } else {
+      xbuf[wave * 64 + lane] = v;
+    }
+  };
+  auto xget = [&](int slot) -> f32x4 {
+    if constexpr (kShared) {
+      const float *x = (const float *)xbuf;
+      return f32x4{x[(slot * 4 + 0) * 64 + lane], x[(slot * 4 + 1) * 64 + lane],
+                   x[(slot * 4 + 2) * 64 + lane], x[(slot * 4 + 3) * 64 + lane]};
+    } else {
+      return xbuf[slot * 64 + lane];
+    }
+  };
   // the group's partial S^T, added in a fixed order (after the exchange)
   auto reduce = [&](f32x4 (&sacc)[2]) {
     const int base = hg * FS;
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      f32x4 c = xbuf[(base + b) * 64 + lane];
+      f32x4 c = xget(base + b);
 #pragma unroll
-      for (int pp = 1; pp < R::kParts; ++pp) c += xbuf[(base + b + 2 * pp) * 64 + lane];
+      for (int pp = 1; pp < R::kParts; ++pp) c += xget(base + b + 2 * pp);
       sacc[b] = c;
     }
   };
@@ -404,9 +426,9 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
     const float c = p.scale_log2;
     // this lane's score of value v: the partials added in the order reduce() uses
     const float *x = (const float *)xbuf;
-    float sc = x[(b * 64 + lane) * 4 + k];
+    float sc = x[(b * 4 + k) * 64 + lane];
 #pragma unroll
-    for (int pp = 1; pp < R::kParts; ++pp) sc += x[((b + 2 * pp) * 64 + lane) * 4 + k];
+    for (int pp = 1; pp < R::kParts; ++pp) sc += x[((b + 2 * pp) * 4 + k) * 64 + lane];
     const bool valid = ((vmask >> (b * 16 + kbase + 2 * k)) & 1u) != 0;
     auto publish = [&](float d, bool flag) {
       const float pv = fast_exp2(d);
@@ -512,7 +534,7 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
     f32x4 sacc[2];
     scores(st_ckv, sacc);
     if (i > 0) pv(lds + ((i - 1) % kStages) * kStageBytes, p_hi, p_lo);
-    if (FS >= 2) xbuf[wave * 64 + lane] = sacc[0];
+    if (FS >= 2) xput(sacc[0]);
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): partial written, tile i-1 read
     __builtin_amdgcn_s_barrier();
     if (i + kStages - 1 < n_tiles) issue_tile(i + kStages - 1);
