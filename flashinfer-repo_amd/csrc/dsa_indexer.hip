@@ -395,35 +395,37 @@ __device__ __forceinline__ void emit_pos(const IndexerParams &p, int t, int32_t 
   out[rank] = v;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave: row shifts within rows
+// of 16 lanes, then the row totals carried with the row broadcasts (gfx9
+// wave64 DPP; lanes without a source add 0).
+__device__ __forceinline__ int wave_inclusive_sum(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2, 3
+  return v;
+}
+
 // Exclusive prefix sums of (a, b) over the 1024 threads of the block; the
-// totals go to *ta, *tb.
+// totals go to *ta, *tb.  Wave sums, then wave 0 scans the 16 wave totals.
 __device__ int2 block_exclusive_scan2(int a, int b, int2 *scratch, int *ta, int *tb) {
+  constexpr int kWaves = kTopkThreads / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int x = a, y = b;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int xu = __shfl_up(x, o), yu = __shfl_up(y, o);
-    if (lane >= o) {
-      x += xu;
-      y += yu;
-    }
-  }
+  const int x = wave_inclusive_sum(a), y = wave_inclusive_sum(b);
   if (lane == 63) scratch[wave] = make_int2(x, y);
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int ra = 0, rbv = 0;
-    for (int w = 0; w < kTopkThreads / 64; ++w) {
-      const int2 c = scratch[w];
-      scratch[w] = make_int2(ra, rbv);
-      ra += c.x;
-      rbv += c.y;
-    }
-    scratch[kTopkThreads / 64] = make_int2(ra, rbv);
+  if (wave == 0) {
+    const int2 w = lane < kWaves ? scratch[lane] : make_int2(0, 0);
+    const int ix = wave_inclusive_sum(w.x), iy = wave_inclusive_sum(w.y);
+    if (lane < kWaves) scratch[lane] = make_int2(ix - w.x, iy - w.y);
+    if (lane == kWaves - 1) scratch[kWaves] = make_int2(ix, iy);
   }
   __syncthreads();
   const int2 base = scratch[wave];
-  *ta = scratch[kTopkThreads / 64].x;
-  *tb = scratch[kTopkThreads / 64].y;
+  *ta = scratch[kWaves].x;
+  *tb = scratch[kWaves].y;
   __syncthreads();
   return make_int2(base.x + x - a, base.y + y - b);
 }
@@ -455,19 +457,27 @@ __device__ __forceinline__ void pick_digit(const uint32_t *tot, uint32_t prefix,
   }
 }
 
-// Shared state of one top-k workgroup.  After the radix passes the histogram
-// space holds the row's keys (KEYS of them, one pad word per 32) for the
-// ordered compaction.
+// Survivors of the first two radix passes that the register top-k ranks
+// directly; more take two more passes.
+constexpr int kMaxSurvivors = 256;
+
+// Shared state of one top-k workgroup (KEYS = positions it holds).  One
+// space serves the radix histograms and then the selected positions by
+// rank.  The bitmaps hold one bit per position: 64-bit word e*16 + w covers
+// positions e*1024 + 64w .. +63, i.e. the keys e of wave w's 64 lanes.
 template <int KEYS>
 struct TopkShared {
   union {
     uint32_t hist[kHistCopies * kHistPitch];
-    uint32_t keys[KEYS + KEYS / 32];
+    int32_t pos[KEYS];
   };
+  uint64_t bits[KEYS / 64 > 0 ? KEYS / 64 : 1];    // selected
+  uint64_t eqbits[KEYS / 64 > 0 ? KEYS / 64 : 1];  // ties of the k-th key
+  uint2 cand[kMaxSurvivors];                       // (key, position), any order
   uint32_t tot[256];
   int2 scan[kTopkThreads / 64 + 1];
   uint32_t prefix, mask;
-  int need;
+  int need, n_cand;
 };
 
 // Rows with at most topk candidates: every candidate, then -1.
@@ -484,9 +494,12 @@ __device__ __forceinline__ bool take_all(const IndexerParams &p, int t, int32_t 
 // the prefix (everything else is counted in the spare bin 256 of each copy,
 // so the atomics need no branch), then the digit of the need-th largest.
 // for_keys(f) calls f(key, is_candidate) for each of this thread's keys.
+// `phantom` keys of value 0 that are not candidates were counted too (they
+// sit in bin 0 while the prefix is 0) and are taken out of that bin.
 template <typename Shared, typename ForKeys>
 __device__ __forceinline__ void radix_pass(Shared &sh, int shift, ForKeys for_keys,
-                                           uint32_t &prefix, uint32_t &mask, int &need) {
+                                           uint32_t &prefix, uint32_t &mask, int &need,
+                                           int phantom = 0) {
   for (int i = threadIdx.x; i < kHistCopies * kHistPitch; i += kTopkThreads) sh.hist[i] = 0;
   __syncthreads();
   uint32_t *myhist = sh.hist + (threadIdx.x & (kHistCopies - 1)) * kHistPitch;
@@ -500,6 +513,42 @@ __device__ __forceinline__ void radix_pass(Shared &sh, int shift, ForKeys for_ke
     uint32_t c = 0;
 #pragma unroll 8
     for (int j = 0; j < kHistCopies; ++j) c += sh.hist[j * kHistPitch + threadIdx.x];
+    if (threadIdx.x == 0 && prefix == 0) c -= (uint32_t)phantom;
+    sh.tot[threadIdx.x] = c;
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) pick_digit(sh.tot, prefix, mask, shift, need, &sh.prefix, &sh.mask, &sh.need);
+  __syncthreads();
+  prefix = sh.prefix;
+  mask = sh.mask;
+  need = sh.need;
+}
+
+// Key of the positions past a row's candidates in the register top-k: the
+// buffer load reads them as 0.0.
+constexpr uint32_t kPhantomKey = 0x80000000u;
+
+// One radix pass over the register-resident keys of a row.  Under prefix pf
+// (the digits above `shift` fixed so far) a key's digit is (k - pf) >> shift
+// when it matches the prefix (then below 256) and at least 256 otherwise, so
+// min(., 256) files every other key in the spare bin with three instructions
+// per key.  The `phantom` copies of kPhantomKey are taken out of their bin.
+template <int EPT, typename Shared>
+__device__ __forceinline__ void radix_pass_regs(Shared &sh, int shift, const uint32_t (&key)[EPT],
+                                                uint32_t &prefix, uint32_t &mask, int &need,
+                                                int phantom) {
+  for (int i = threadIdx.x; i < kHistCopies * kHistPitch; i += kTopkThreads) sh.hist[i] = 0;
+  __syncthreads();
+  uint32_t *myhist = sh.hist + (threadIdx.x & (kHistCopies - 1)) * kHistPitch;
+  const uint32_t pf = prefix;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) atomicAdd(&myhist[min((key[e] - pf) >> shift, 256u)], 1u);
+  __syncthreads();
+  if (threadIdx.x < 256) {
+    uint32_t c = 0;
+#pragma unroll 8
+    for (int j = 0; j < kHistCopies; ++j) c += sh.hist[j * kHistPitch + threadIdx.x];
+    if (threadIdx.x == min((kPhantomKey - pf) >> shift, 256u)) c -= (uint32_t)phantom;
     sh.tot[threadIdx.x] = c;
   }
   __syncthreads();
@@ -512,60 +561,170 @@ __device__ __forceinline__ void radix_pass(Shared &sh, int shift, ForKeys for_ke
 
 template <int EPT>
 __global__ __launch_bounds__(kTopkThreads) void dsa_idx_topk_kernel(IndexerParams p) {
-  static_assert(EPT <= 32, "selection masks and the LDS key stage hold 32 keys per thread");
-  __shared__ TopkShared<EPT * kTopkThreads> sh;
+  static_assert(EPT <= 32, "one 32-bit bitmap word per thread at most");
+  constexpr int KEYS = EPT * kTopkThreads;
+  static_assert(KEYS <= 32768, "survivor ranks pack positions in 15 bits");
+  constexpr int kWaves = kTopkThreads / 64;
+  __shared__ TopkShared<KEYS> sh;
   const int t = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // known uniform: scalar masks
   const float *row = p.scores + (int64_t)t * p.S;
   int32_t *out = p.out + (int64_t)t * p.topk;
   const int n = max(0, min(p.S, p.limit[t] + 1));  // candidates 0..n-1
   if (take_all(p, t, out, n)) return;               // n > topk >= 1 below
 
-  // radix passes: key e of this thread is position e*1024 + tid (coalesced)
+  // Key e of this thread is position e*1024 + tid (coalesced), so the 64
+  // lanes of a wave hold 64 consecutive positions of every e.  A buffer load
+  // over the n candidates needs one 32-bit offset register for all 32 loads
+  // (kept in flight together) and reads the positions past n as 0.0: those
+  // `phantom` keys are taken out of the histograms and masked out of the
+  // selection by position, which is uniform per wave and e.  Adding +0.0
+  // turns -0.0 into +0.0; the key orders the scores as unsigned integers.
   uint32_t key[EPT];
+  {
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(row), 0, n * 4, 0x00020000);
 #pragma unroll
-  for (int e = 0; e < EPT; ++e) key[e] = order_key(row[min(e * kTopkThreads + (int)threadIdx.x, n - 1)]);
+    for (int e = 0; e < EPT; ++e) {
+      const float f = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(rs, tid * 4, e * kTopkThreads * 4, 0));
+      const uint32_t u = __builtin_bit_cast(uint32_t, f + 0.0f);
+      key[e] = u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
+    }
+  }
+  const int phantom = KEYS - n;
+  auto valid64 = [&](int e) {  // this wave's positions of key e that are below n
+    const int c = n - (e * kTopkThreads + wave * 64);
+    return c >= 64 ? ~0ull : (c <= 0 ? 0ull : (1ull << c) - 1ull);
+  };
+  if (tid == 0) sh.n_cand = 0;  // ordered before its use by the passes' barriers
 
+  // Two passes: the k-th largest key lies in the 16-bit bin `prefix`; keys
+  // above the bin are all taken and `need` more come from its survivors.
   uint32_t prefix = 0, mask = 0;
-  int need = p.topk;
-  for (int shift = 24; shift >= 0; shift -= 8)
-    radix_pass(sh, shift,
-               [&](auto f) {
+  int need = p.topk, unused;
+#pragma unroll 1
+  for (int shift = 24; shift >= 16; shift -= 8)
+    radix_pass_regs(sh, shift, key, prefix, mask, need, phantom);
+
+  // Selection as a position bitmap, built from ballots of the registers
+  // (64-bit word e*16 + wave holds key e of the wave's lanes); the bin's
+  // survivors are listed (key, position) for an exact ranking.
+  uint32_t *bits32 = (uint32_t *)sh.bits;  // word w: positions 32w .. 32w+31
+  {
+    const uint32_t hi = prefix | 0xffffu;  // keys above the bin
 #pragma unroll
-                 for (int e = 0; e < EPT; ++e) f(key[e], e * kTopkThreads + (int)threadIdx.x < n);
-               },
-               prefix, mask, need);
-  // prefix is now the k-th largest key; `need` of its ties are taken, lowest
-  // positions first.  The keys move through LDS so that each thread then
-  // owns a contiguous run of positions [tid*EPT, tid*EPT + EPT).
-#pragma unroll
-  for (int e = 0; e < EPT; ++e) {
-    const int pos = e * kTopkThreads + threadIdx.x;
-    sh.keys[pos + (pos >> 5)] = key[e];
+    for (int e = 0; e < EPT; ++e) {
+      const uint64_t vm = valid64(e);
+      const uint64_t ab = __ballot(key[e] > hi) & vm;
+      const uint64_t sb = __ballot(key[e] - prefix < 0x10000u) & vm;
+      if (lane == 0) sh.bits[e * kWaves + wave] = ab;
+      if (sb != 0) {
+        int o = 0;
+        if (lane == 0) o = atomicAdd(&sh.n_cand, __popcll(sb));
+        o = __builtin_amdgcn_readfirstlane(o) +
+            __builtin_amdgcn_mbcnt_hi((uint32_t)(sb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)sb, 0));
+        if (((sb >> lane) & 1) && o < kMaxSurvivors)
+          sh.cand[o] = make_uint2(key[e], (uint32_t)(e * kTopkThreads + tid));
+      }
+    }
   }
   __syncthreads();
-  const int base = threadIdx.x * EPT;
-  const int nv = max(0, min(EPT, n - base));
-  uint32_t gt = 0, eq = 0;
+  const int n_surv = sh.n_cand;
+  if (n_surv <= kMaxSurvivors) {  // uniform
+    // Rank: key descending, position ascending.  Survivors share the top 16
+    // key bits, so (low 16 bits, 32767 - position) orders them as a 31-bit
+    // value; up to 64 survivors one wave finds the need-th largest bit by
+    // bit with ballots, more walk all pairs with readlane.
+    if (n_surv <= 64) {
+      if (wave == 0) {
+        const bool act = lane < n_surv;
+        const uint2 me = sh.cand[min(lane, n_surv - 1)];
+        const uint32_t c = ((me.x & 0xffffu) << 15) | (uint32_t)(32767 - (int)me.y);
+        uint32_t thr = 0;
+        int k = need;
+        for (int bit = 30; bit >= 0; --bit) {
+          const uint64_t ones =
+              __ballot(act && (c >> (bit + 1)) == (thr >> (bit + 1)) && ((c >> bit) & 1u));
+          const int cnt = __popcll(ones);
+          if (cnt >= k) thr |= 1u << bit;
+          else k -= cnt;
+        }
+        if (act && c >= thr) atomicOr(&bits32[me.y >> 5], 1u << (me.y & 31));
+      }
+    } else if (tid < ((n_surv + 63) & ~63)) {  // uniform per wave
+      const uint2 me = sh.cand[min(tid, n_surv - 1)];
+      int rank = 0;
+      for (int c = 0; c < n_surv; c += 64) {
+        const uint2 other = sh.cand[min(c + lane, n_surv - 1)];
+        const int m = min(64, n_surv - c);
+        for (int j = 0; j < m; ++j) {
+          const uint32_t ok = __builtin_amdgcn_readlane(other.x, j);
+          const uint32_t op = __builtin_amdgcn_readlane(other.y, j);
+          rank += (ok > me.x) || (ok == me.x && op < me.y);
+        }
+      }
+      if (tid < n_surv && rank < need) atomicOr(&bits32[me.y >> 5], 1u << (me.y & 31));
+    }
+    __syncthreads();
+  } else {
+    // Many keys share the bin: two more passes pin the k-th key itself;
+    // keys above it are taken, and `need` of its ties, lowest positions first.
+#pragma unroll 1
+    for (int shift = 8; shift >= 0; shift -= 8)
+      radix_pass_regs(sh, shift, key, prefix, mask, need, phantom);
 #pragma unroll
-  for (int e = 0; e < EPT; ++e) {
-    const int pos = base + e;
-    const uint32_t k = sh.keys[pos + (pos >> 5)];
-    gt |= (uint32_t)(e < nv && k > prefix) << e;
-    eq |= (uint32_t)(e < nv && k == prefix) << e;
+    for (int e = 0; e < EPT; ++e) {
+      const uint64_t vm = valid64(e);
+      const uint64_t gb = __ballot(key[e] > prefix) & vm;
+      const uint64_t qb = __ballot(key[e] == prefix) & vm;
+      if (lane == 0) {
+        sh.bits[e * kWaves + wave] = gb;
+        sh.eqbits[e * kWaves + wave] = qb;
+      }
+    }
+    __syncthreads();
+    uint32_t eq = tid < KEYS / 32 ? ((const uint32_t *)sh.eqbits)[tid] : 0u;
+    int tot_eq;
+    const int2 ex = block_exclusive_scan2(__builtin_popcount(eq), 0, sh.scan, &tot_eq, &unused);
+    uint32_t take = 0;
+    for (int left = need - ex.x; left > 0 && eq != 0; --left) {
+      take |= eq & (~eq + 1);
+      eq &= eq - 1;
+    }
+    if (take != 0) bits32[tid] |= take;  // this thread's own word
   }
-  int tot_gt, tot_eq;
-  const int2 ex = block_exclusive_scan2(__builtin_popcount(gt), __builtin_popcount(eq), sh.scan,
-                                        &tot_gt, &tot_eq);
-  uint32_t sel = gt;
-  for (int left = need - ex.y; left > 0 && eq != 0; --left) {  // lowest ties first
-    sel |= eq & (~eq + 1);
-    eq &= eq - 1;
-  }
-  int o = ex.x + min(ex.y, need);
+
+  // Output ranks in position order: thread tid owns bitmap word tid; the
+  // selected positions go to LDS by rank (the scan's barriers order this
+  // after every bitmap read), then each thread maps up to four of them
+  // through the block table with the loads issued together and stores them
+  // coalesced.
+  uint32_t sel = tid < KEYS / 32 ? bits32[tid] : 0u;
+  int n_sel;
+  const int2 rx = block_exclusive_scan2(__builtin_popcount(sel), 0, sh.scan, &n_sel, &unused);
+  int o = rx.x;
   while (sel != 0) {
     const int e = __builtin_ctz(sel);
     sel &= sel - 1;
-    emit_pos(p, t, out, base + e, o++);
+    sh.pos[o++] = tid * 32 + e;
+  }
+  __syncthreads();
+  for (int r0 = tid; r0 < p.topk; r0 += 4 * kTopkThreads) {
+    int v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = sh.pos[min(r0 + u * kTopkThreads, p.topk - 1)];
+    if (p.block_table != nullptr) {
+      const int32_t *bt = p.block_table + (int64_t)t * p.bt_stride;
+      int page[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) page[u] = bt[v[u] / p.page_size];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = page[u] * p.page_size + v[u] % p.page_size;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (r0 + u * kTopkThreads < p.topk) out[r0 + u * kTopkThreads] = v[u];
   }
 }
 

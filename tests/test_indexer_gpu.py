@@ -89,6 +89,35 @@ def test_ties_go_to_lower_positions():
     assert np.array_equal(got_idx, np.tile(np.arange(50, dtype=np.int32), (4, 1)))
 
 
+@pytest.mark.parametrize("n_tied,topk", [(40, 30), (150, 100), (300, 200), (150, 150)])
+def test_tied_top_group_every_selection_path(n_tied, topk):
+    """The top `n_tied` scores of each row are exactly equal (identical key
+    rows) and the k-th largest lies among them: the register top-k then
+    ranks up to 64 survivors with ballots, up to 256 pairwise, and more
+    takes two further radix passes.  Every path must take the lowest
+    positions of the tie."""
+    g = torch.Generator().manual_seed(n_tied)
+    T, Hi, S = 3, 16, 4096
+    q = torch.ones(T, Hi, 128)
+    k = torch.randn(S, 128, generator=g)
+    k[:n_tied] = 2.0                                   # dot = 256 against ~N(0, 11)
+    perm = torch.randperm(S, generator=g)             # spread the tied rows over the row
+    k = k[perm]
+    d = {"q_idx": workloads.e4m3(q), "k_idx": workloads.e4m3(k),
+         "k_scale": torch.ones(S), "weights": torch.full((T, Hi), 1.0 / Hi),
+         "causal_limit": torch.tensor([S - 1, S - 7, S - 1000], dtype=torch.int32)}
+    got_idx, got_sc = _gpu_indexer(d, topk)
+    ref_idx, ref_sc = _oracle(d, topk)
+    _assert_same(got_idx, got_sc, ref_idx, ref_sc, f"tied group {n_tied}, k={topk}")
+    tied_pos = np.sort(np.flatnonzero(np.isin(perm.numpy(), np.arange(n_tied))))
+    for t in range(T):
+        n = int(d["causal_limit"][t]) + 1
+        want = tied_pos[tied_pos < n][:topk]           # the lowest tied positions win
+        assert np.isin(want, got_idx[t]).all(), f"row {t}"
+        if len(want) == topk:
+            assert np.array_equal(got_idx[t], want), f"row {t}"
+
+
 def test_large_values_take_the_wide_paths():
     """|value| >= 32 needs the third 7-bit piece (fp64 combine), and large
     dots overflow the int32 fast combine; both must stay exact."""
