@@ -435,21 +435,18 @@ __device__ int2 block_exclusive_scan2(int a, int b, int2 *scratch, int *ta, int 
 __device__ __forceinline__ void pick_digit(const uint32_t *tot, uint32_t prefix, uint32_t mask,
                                            int shift, int need, uint32_t *s_prefix,
                                            uint32_t *s_mask, int *s_need) {
-  const int l = threadIdx.x;  // 0..63, lane l owns bins 4l..4l+3
-  const uint32_t c0 = tot[4 * l], c1 = tot[4 * l + 1], c2 = tot[4 * l + 2], c3 = tot[4 * l + 3];
+  // Lane l owns bins b0 .. b0+3 with b0 = 4*(63 - l), so the bins above
+  // its own belong to lanes 0..l-1: their count is an exclusive prefix sum.
+  const int l = threadIdx.x;
+  const int b0 = 4 * (63 - l);
+  const uint32_t c0 = tot[b0], c1 = tot[b0 + 1], c2 = tot[b0 + 2], c3 = tot[b0 + 3];
   const uint32_t local = c0 + c1 + c2 + c3;
-  uint32_t x = local;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t y = __shfl_down(x, o);
-    if (l + o < 64) x += y;
-  }
-  uint32_t cum = x - local;  // keys in the bins above this lane's
+  uint32_t cum = (uint32_t)wave_inclusive_sum((int)local) - local;  // keys in the bins above
   const uint32_t cs[4] = {c0, c1, c2, c3};
 #pragma unroll
   for (int b = 3; b >= 0; --b) {
     if ((int)cum < need && (int)(cum + cs[b]) >= need) {
-      *s_prefix = prefix | ((uint32_t)(4 * l + b) << shift);
+      *s_prefix = prefix | ((uint32_t)(b0 + b) << shift);
       *s_mask = mask | (255u << shift);
       *s_need = need - (int)cum;
     }
@@ -593,10 +590,6 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_idx_topk_kernel(IndexerParam
     }
   }
   const int phantom = KEYS - n;
-  auto valid64 = [&](int e) {  // this wave's positions of key e that are below n
-    const int c = n - (e * kTopkThreads + wave * 64);
-    return c >= 64 ? ~0ull : (c <= 0 ? 0ull : (1ull << c) - 1ull);
-  };
   if (tid == 0) sh.n_cand = 0;  // ordered before its use by the passes' barriers
 
   // Two passes: the k-th largest key lies in the 16-bit bin `prefix`; keys
@@ -608,63 +601,59 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_idx_topk_kernel(IndexerParam
     radix_pass_regs(sh, shift, key, prefix, mask, need, phantom);
 
   // Selection as a position bitmap, built from ballots of the registers
-  // (64-bit word e*16 + wave holds key e of the wave's lanes); the bin's
-  // survivors are listed (key, position) for an exact ranking.
+  // (64-bit word e*16 + wave holds key e of the wave's lanes: lane 2e + h
+  // collects half h and one store per lane writes them).  Positions past n
+  // are masked out when the words are read.  Waves holding survivors of the
+  // bin list them (key, position) for an exact ranking.
   uint32_t *bits32 = (uint32_t *)sh.bits;  // word w: positions 32w .. 32w+31
   {
     const uint32_t hi = prefix | 0xffffu;  // keys above the bin
+    uint32_t bw = 0;
+    uint64_t any = 0;
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
-      const uint64_t vm = valid64(e);
-      const uint64_t ab = __ballot(key[e] > hi) & vm;
-      const uint64_t sb = __ballot(key[e] - prefix < 0x10000u) & vm;
-      if (lane == 0) sh.bits[e * kWaves + wave] = ab;
-      if (sb != 0) {
-        int o = 0;
-        if (lane == 0) o = atomicAdd(&sh.n_cand, __popcll(sb));
-        o = __builtin_amdgcn_readfirstlane(o) +
-            __builtin_amdgcn_mbcnt_hi((uint32_t)(sb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)sb, 0));
-        if (((sb >> lane) & 1) && o < kMaxSurvivors)
-          sh.cand[o] = make_uint2(key[e], (uint32_t)(e * kTopkThreads + tid));
+      const uint64_t ab = __ballot(key[e] > hi);
+      any |= __ballot(key[e] - prefix < 0x10000u);
+      bw = lane == 2 * e ? (uint32_t)ab : bw;
+      bw = lane == 2 * e + 1 ? (uint32_t)(ab >> 32) : bw;
+    }
+    if (lane < 2 * EPT) bits32[((lane >> 1) * kWaves + wave) * 2 + (lane & 1)] = bw;
+    if (any != 0) {  // uniform
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const uint64_t sb = __ballot(key[e] - prefix < 0x10000u);
+        if (sb != 0) {
+          int o = 0;
+          if (lane == 0) o = atomicAdd(&sh.n_cand, __popcll(sb));
+          o = __builtin_amdgcn_readfirstlane(o) +
+              __builtin_amdgcn_mbcnt_hi((uint32_t)(sb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)sb, 0));
+          if (((sb >> lane) & 1) && o < kMaxSurvivors)
+            sh.cand[o] = make_uint2(key[e], (uint32_t)(e * kTopkThreads + tid));
+        }
       }
     }
   }
   __syncthreads();
   const int n_surv = sh.n_cand;
   if (n_surv <= kMaxSurvivors) {  // uniform
-    // Rank: key descending, position ascending.  Survivors share the top 16
-    // key bits, so (low 16 bits, 32767 - position) orders them as a 31-bit
-    // value; up to 64 survivors one wave finds the need-th largest bit by
-    // bit with ballots, more walk all pairs with readlane.
-    if (n_surv <= 64) {
-      if (wave == 0) {
-        const bool act = lane < n_surv;
-        const uint2 me = sh.cand[min(lane, n_surv - 1)];
-        const uint32_t c = ((me.x & 0xffffu) << 15) | (uint32_t)(32767 - (int)me.y);
-        uint32_t thr = 0;
-        int k = need;
-        for (int bit = 30; bit >= 0; --bit) {
-          const uint64_t ones =
-              __ballot(act && (c >> (bit + 1)) == (thr >> (bit + 1)) && ((c >> bit) & 1u));
-          const int cnt = __popcll(ones);
-          if (cnt >= k) thr |= 1u << bit;
-          else k -= cnt;
+    // Rank: key descending, position ascending, among the survivors below n
+    // (the list may hold positions past n).  Four lanes per survivor each
+    // count the survivors ahead of it in a quarter of the list, and two DPP
+    // quad swaps add the counts; the first `need` are marked.
+    {
+      const int i = tid >> 2, q = tid & 3;
+      if (i < ((n_surv + 15) & ~15)) {  // whole waves
+        const uint2 me = sh.cand[min(i, n_surv - 1)];
+        int r = 0;
+        for (int j = q; j < n_surv; j += 4) {
+          const uint2 c = sh.cand[j];
+          r += (int)c.y < n && (c.x > me.x || (c.x == me.x && c.y < me.y));
         }
-        if (act && c >= thr) atomicOr(&bits32[me.y >> 5], 1u << (me.y & 31));
+        r += __builtin_amdgcn_update_dpp(0, r, 0xb1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
+        r += __builtin_amdgcn_update_dpp(0, r, 0x4e, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+        if (q == 0 && i < n_surv && (int)me.y < n && r < need)
+          atomicOr(&bits32[me.y >> 5], 1u << (me.y & 31));
       }
-    } else if (tid < ((n_surv + 63) & ~63)) {  // uniform per wave
-      const uint2 me = sh.cand[min(tid, n_surv - 1)];
-      int rank = 0;
-      for (int c = 0; c < n_surv; c += 64) {
-        const uint2 other = sh.cand[min(c + lane, n_surv - 1)];
-        const int m = min(64, n_surv - c);
-        for (int j = 0; j < m; ++j) {
-          const uint32_t ok = __builtin_amdgcn_readlane(other.x, j);
-          const uint32_t op = __builtin_amdgcn_readlane(other.y, j);
-          rank += (ok > me.x) || (ok == me.x && op < me.y);
-        }
-      }
-      if (tid < n_surv && rank < need) atomicOr(&bits32[me.y >> 5], 1u << (me.y & 31));
     }
     __syncthreads();
   } else {
@@ -673,11 +662,12 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_idx_topk_kernel(IndexerParam
 #pragma unroll 1
     for (int shift = 8; shift >= 0; shift -= 8)
       radix_pass_regs(sh, shift, key, prefix, mask, need, phantom);
+    // (Ties past n sit after every real position and `need` counts real
+    // ones only, so they are never taken; the masking below clears the rest.)
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
-      const uint64_t vm = valid64(e);
-      const uint64_t gb = __ballot(key[e] > prefix) & vm;
-      const uint64_t qb = __ballot(key[e] == prefix) & vm;
+      const uint64_t gb = __ballot(key[e] > prefix);
+      const uint64_t qb = __ballot(key[e] == prefix);
       if (lane == 0) {
         sh.bits[e * kWaves + wave] = gb;
         sh.eqbits[e * kWaves + wave] = qb;
@@ -700,7 +690,9 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_idx_topk_kernel(IndexerParam
   // after every bitmap read), then each thread maps up to four of them
   // through the block table with the loads issued together and stores them
   // coalesced.
+  const int nw = n - tid * 32;  // this word's positions below n
   uint32_t sel = tid < KEYS / 32 ? bits32[tid] : 0u;
+  sel &= nw >= 32 ? ~0u : (nw <= 0 ? 0u : (1u << nw) - 1u);
   int n_sel;
   const int2 rx = block_exclusive_scan2(__builtin_popcount(sel), 0, sh.scan, &n_sel, &unused);
   int o = rx.x;
