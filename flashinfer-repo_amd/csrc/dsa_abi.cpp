@@ -309,6 +309,8 @@ IndexerWorkspace indexer_workspace_layout(int64_t T, int64_t Hi, int64_t S, bool
   off += up256(qblocks * 3 * 2 * 1024);
   w.q_max = off;
   off += up256(qblocks * 4);
+  w.k_scale = off;
+  off += up256((size_t)S * 4);
   w.scores = off;
   if (own_scores) off += up256((size_t)T * (size_t)S * 4);
   w.total = off;
@@ -338,12 +340,19 @@ int dsa_indexer_topk(const dsa_indexer_args *a, void *stream) {
       a->num_tokens * a->num_positions > (1LL << 40))
     return fail(DSA_EUNSUPPORTED, "%s: size beyond the supported range", fn);
   if (a->num_tokens == 0) return ok();
+  const bool paged = a->k_cache != nullptr;
+  if (paged && (a->k_idx || a->k_scale))
+    return fail(DSA_EINVAL, "%s: give k_idx/k_scale or k_cache, not both", fn);
+  if (paged && (!a->k_pages || a->k_page_size <= 0 || a->k_page_size % 4 != 0 ||
+                a->k_page_size > (1 << 24)))
+    return fail(DSA_EINVAL, "%s: k_cache needs k_pages and a k_page_size that is a positive "
+                "multiple of 4 (got %lld)", fn, (long long)a->k_page_size);
   if (!a->q_idx || !a->weights || !a->causal_limit || (a->topk > 0 && !a->out) ||
-      (a->num_positions > 0 && (!a->k_idx || !a->k_scale)))
+      (a->num_positions > 0 && !paged && (!a->k_idx || !a->k_scale)))
     return fail(DSA_EINVAL, "%s: NULL tensor pointer", fn);
   if (!aligned(a->q_idx, 16) || !aligned(a->k_idx, 16) || !aligned(a->k_scale, 4) ||
       !aligned(a->weights, 4) || !aligned(a->causal_limit, 4) || !aligned(a->out, 4) ||
-      !aligned(a->scores_out, 4))
+      !aligned(a->scores_out, 4) || !aligned(a->k_cache, 16) || !aligned(a->k_pages, 4))
     return fail(DSA_EINVAL, "%s: misaligned pointer (e4m3 rows need 16 bytes)", fn);
   if (a->block_table && (a->page_size <= 0 || a->block_table_stride < 0))
     return fail(DSA_EINVAL, "%s: block_table needs page_size > 0 and a stride >= 0", fn);
@@ -372,8 +381,42 @@ int dsa_indexer_topk(const dsa_indexer_args *a, void *stream) {
   p.k_max = reinterpret_cast<int32_t *>(ws + lay.k_max);
   p.q_pieces = reinterpret_cast<int8_t *>(ws + lay.q_pieces);
   p.q_max = reinterpret_cast<int32_t *>(ws + lay.q_max);
+  if (paged) {
+    p.k_cache = a->k_cache;
+    p.k_pages = a->k_pages;
+    p.k_page_size = (int32_t)a->k_page_size;
+    p.k_scale_ws = reinterpret_cast<float *>(ws + lay.k_scale);
+    p.k_scale = p.k_scale_ws;
+  }
   p.scores = a->scores_out ? a->scores_out : reinterpret_cast<float *>(ws + lay.scores);
   const hipError_t e = dsa::launch_indexer(p, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(DSA_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
+  return ok();
+}
+
+int dsa_indexer_k_append(const dsa_k_append_args *a, void *stream) {
+  const char *fn = "dsa_indexer_k_append";
+  if (!a) return fail(DSA_EINVAL, "%s: args is NULL", fn);
+  if (a->num_tokens < 0 || a->num_pages < 0 || a->page_size <= 0 || a->page_size % 4 != 0)
+    return fail(DSA_EINVAL, "%s: need num_tokens, num_pages >= 0 and a page_size that is a "
+                "positive multiple of 4 (got %lld, %lld, %lld)", fn, (long long)a->num_tokens,
+                (long long)a->num_pages, (long long)a->page_size);
+  if (a->num_tokens > 0x7fffffffLL || a->num_pages * a->page_size > 0x7fffffffLL)
+    return fail(DSA_EUNSUPPORTED, "%s: size beyond the supported range", fn);
+  if (a->num_tokens == 0) return ok();
+  if (!a->k || !a->slots || !a->k_cache) return fail(DSA_EINVAL, "%s: NULL tensor pointer", fn);
+  if (a->k_stride < kIndexerHeadDim || (a->k_stride * 2) % 16 != 0 || !aligned(a->k, 16) ||
+      !aligned(a->slots, 4) || !aligned(a->k_cache, 16))
+    return fail(DSA_EINVAL, "%s: rows and k_cache must be 16-byte aligned (stride >= 128)", fn);
+  dsa::KAppendParams p = {};
+  p.k = static_cast<const uint16_t *>(a->k);
+  p.k_stride = a->k_stride;
+  p.slots = a->slots;
+  p.n = (int32_t)a->num_tokens;
+  p.cache = a->k_cache;
+  p.num_slots = a->num_pages * a->page_size;
+  p.page_size = (int32_t)a->page_size;
+  const hipError_t e = dsa::launch_k_append(p, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(DSA_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
   return ok();
 }

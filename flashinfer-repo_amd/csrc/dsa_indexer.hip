@@ -64,6 +64,7 @@ namespace {
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kIdxDim = 128;
+constexpr int kKTokenBytes = kIdxDim + 4;  // paged K cache: codes + fp32 scale per token
 constexpr int kChunk = 1024;              // one MFMA operand: 64 lanes x 16 bytes
 constexpr int kBlockBytes = 3 * 2 * kChunk;
 constexpr int kPrepThreads = 256;         // two 16-row blocks x 8 segments of 16 bytes
@@ -130,7 +131,16 @@ __global__ __launch_bounds__(kPrepThreads) void dsa_idx_prep_kernel(IndexerParam
   if (active) {
     if (is_k) {
       const int s = rb * 16 + r;
-      if (s < p.S) raw = *(const uint4 *)(p.k + (int64_t)s * kIdxDim + seg * 16);
+      if (s < p.S) {
+        if (p.k_cache != nullptr) {  // paged: codes, and the scale copied to the workspace
+          const int pg = p.k_pages[s / p.k_page_size], off = s % p.k_page_size;
+          const uint8_t *page = p.k_cache + (int64_t)pg * p.k_page_size * kKTokenBytes;
+          raw = *(const uint4 *)(page + off * kIdxDim + seg * 16);
+          if (seg == 0) p.k_scale_ws[s] = *(const float *)(page + p.k_page_size * kIdxDim + off * 4);
+        } else {
+          raw = *(const uint4 *)(p.k + (int64_t)s * kIdxDim + seg * 16);
+        }
+      }
     } else {
       const int qb = rb - nkb;
       t = qb / nqb;
@@ -762,6 +772,45 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_idx_topk_stream_kernel(Index
   }
 }
 
+// ---- quantise-on-append into the paged K cache ---------------------------
+
+// e4m3fn code of x (finite, |x| <= 448), rounded to nearest, ties to even.
+__device__ __forceinline__ uint32_t e4m3_encode(float x) {
+  const uint32_t sign = (__float_as_uint(x) >> 24) & 0x80u;
+  const float a = fabsf(x);
+  uint32_t code;
+  if (a < 0x1p-6f) {  // zero and the subnormals: multiples of 2^-9 (8 = the smallest normal)
+    code = (uint32_t)__builtin_rintf(a * 512.0f);
+  } else {            // 3 mantissa bits, ties to even; exponent rebiased 127 -> 7
+    const uint32_t m = __float_as_uint(a);
+    const uint32_t r = m + 0x7ffffu + ((m >> 20) & 1u);
+    code = (((r >> 23) - 120u) << 3) | ((r >> 20) & 7u);
+  }
+  return sign | code;
+}
+
+// One wave per token: lane l quantises elements 2l, 2l+1.
+__global__ __launch_bounds__(256) void dsa_k_append_kernel(KAppendParams p) {
+  const int lane = threadIdx.x & 63;
+  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (i >= p.n) return;
+  const int slot = p.slots[i];
+  if (slot < 0 || slot >= p.num_slots) return;
+  const uint32_t pair = *(const uint32_t *)(p.k + (int64_t)i * p.k_stride + 2 * lane);
+  const float x0 = __uint_as_float(pair << 16), x1 = __uint_as_float(pair & 0xffff0000u);
+  float amax = fmaxf(fabsf(x0), fabsf(x1));
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  const float scale = fmaxf(amax, 1e-4f) / 448.0f;
+  const float y0 = fminf(fmaxf(x0 / scale, -448.0f), 448.0f);
+  const float y1 = fminf(fmaxf(x1 / scale, -448.0f), 448.0f);
+  const int pg = slot / p.page_size, off = slot - pg * p.page_size;
+  uint8_t *page = p.cache + (int64_t)pg * p.page_size * kKTokenBytes;
+  *(uint16_t *)(page + off * kIdxDim + 2 * lane) =
+      (uint16_t)(e4m3_encode(y0) | (e4m3_encode(y1) << 8));
+  if (lane == 0) *(float *)(page + p.page_size * kIdxDim + off * 4) = scale;
+}
+
 template <int NHB>
 hipError_t launch_score(const IndexerParams &p, dim3 grid, dim3 block, hipStream_t stream) {
   hipLaunchKernelGGL(dsa_idx_score_kernel<NHB>, grid, block, 0, stream, p);
@@ -775,6 +824,12 @@ hipError_t launch_topk(const IndexerParams &p, hipStream_t stream) {
 }
 
 }  // namespace
+
+hipError_t launch_k_append(const KAppendParams &p, hipStream_t stream) {
+  if (p.n == 0) return hipSuccess;
+  hipLaunchKernelGGL(dsa_k_append_kernel, dim3((p.n + 3) / 4), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
 
 hipError_t launch_indexer(const IndexerParams &pin, hipStream_t stream) {
   if (pin.T == 0) return hipSuccess;

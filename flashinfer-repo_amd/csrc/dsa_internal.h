@@ -78,11 +78,19 @@ hipError_t launch_attention_merge(const AttnParams &p, hipStream_t stream);
 //   k_max    [ceil(S/16)]                               max |value * 2^9| per block
 //   q_pieces [T][Hi/16][3 pieces][2 k-steps][1024 B]    MFMA A operands, lane order
 //   q_max    [T][Hi/16]                                 max |value * 2^9| per 16 heads
+//   k_scale  [S] fp32                                   scales gathered from a paged K cache
 //   scores   [T][S] fp32                                (unless the caller's)
 struct IndexerParams {
   const uint8_t *q;       // [T][Hi][128] e4m3 codes
-  const uint8_t *k;       // [S][128] e4m3 codes
-  const float *k_scale;   // [S]
+  const uint8_t *k;       // [S][128] e4m3 codes (or null: paged cache below)
+  const float *k_scale;   // [S] (the workspace copy for a paged cache)
+  // paged K cache: position s is token s % k_page_size of page k_pages[s /
+  // k_page_size]; codes at page*k_page_size*132 + off*128, the fp32 scale at
+  // page*k_page_size*132 + k_page_size*128 + off*4
+  const uint8_t *k_cache;
+  const int32_t *k_pages;
+  int32_t k_page_size;
+  float *k_scale_ws;      // [S] gathered scales (paged cache)
   const float *w;         // [T][Hi]
   const int32_t *limit;   // [T]
   int32_t T, Hi, S, topk;
@@ -99,7 +107,7 @@ struct IndexerParams {
 };
 
 struct IndexerWorkspace {
-  size_t k_pieces, k_max, q_pieces, q_max, scores, total;  // byte offsets; total = size
+  size_t k_pieces, k_max, q_pieces, q_max, k_scale, scores, total;  // byte offsets; total = size
 };
 
 // Offsets of the indexer's workspace regions; scores are left out when the
@@ -107,5 +115,17 @@ struct IndexerWorkspace {
 IndexerWorkspace indexer_workspace_layout(int64_t T, int64_t Hi, int64_t S, bool own_scores);
 
 hipError_t launch_indexer(const IndexerParams &p, hipStream_t stream);
+
+// Quantise-on-append into the paged indexer K cache (layout above).
+struct KAppendParams {
+  const uint16_t *k;  // [n][k_stride] bf16 bits
+  int64_t k_stride;
+  const int32_t *slots;
+  int32_t n;
+  uint8_t *cache;
+  int64_t num_slots;
+  int32_t page_size;
+};
+hipError_t launch_k_append(const KAppendParams &p, hipStream_t stream);
 
 }  // namespace dsa

@@ -16,7 +16,7 @@ DSA_EINVAL = 1
 DSA_EUNSUPPORTED = 2
 DSA_ELAUNCH = 3
 DSA_EWORKSPACE = 4
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 EXPORTED_SYMBOLS = (
     "dsa_attn_fwd",
@@ -27,6 +27,7 @@ EXPORTED_SYMBOLS = (
     "dsa_attn_workspace_bytes",
     "dsa_attn_counter_bytes",
     "dsa_indexer_topk",
+    "dsa_indexer_k_append",
     "dsa_indexer_workspace_bytes",
     "dsa_last_error",
     "dsa_abi_version",
@@ -79,6 +80,16 @@ class IndexerArgs(ctypes.Structure):
         ("block_table", _vp), ("block_table_stride", _i64), ("page_size", _i64),
         ("out", _vp), ("scores_out", _vp),
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+        ("k_cache", _vp), ("k_pages", _vp), ("k_page_size", _i64),
+    ]
+
+
+class KAppendArgs(ctypes.Structure):
+    """Mirror of ``dsa_k_append_args``."""
+
+    _fields_ = [
+        ("k", _vp), ("k_stride", _i64), ("slots", _vp), ("num_tokens", _i64),
+        ("k_cache", _vp), ("num_pages", _i64), ("page_size", _i64),
     ]
 
 
@@ -123,6 +134,8 @@ def load() -> ctypes.CDLL:
     lib.dsa_attn_counter_bytes.restype = ctypes.c_size_t
     lib.dsa_indexer_topk.argtypes = [ctypes.POINTER(IndexerArgs), _vp]
     lib.dsa_indexer_topk.restype = ctypes.c_int
+    lib.dsa_indexer_k_append.argtypes = [ctypes.POINTER(KAppendArgs), _vp]
+    lib.dsa_indexer_k_append.restype = ctypes.c_int
     lib.dsa_indexer_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64]
     lib.dsa_indexer_workspace_bytes.restype = ctypes.c_size_t
     lib.dsa_last_error.argtypes = []

@@ -56,25 +56,52 @@ def run_indexer_and_topk(q_idx: torch.Tensor, k_idx: torch.Tensor, k_scale: torc
     ``block_table[page] * page_size + offset``.  With ``return_scores`` the
     fp32 ``[T, S]`` scores (masked entries -inf) are returned too.
     """
-    q = _codes(q_idx, "q_idx")
     k = _codes(k_idx, "k_idx")
-    _check(q.dim() == 3 and q.shape[2] == INDEX_HEAD_DIM,
-           f"q_idx must be [T, heads, {INDEX_HEAD_DIM}], got {tuple(q.shape)}")
-    T, Hi, _ = q.shape
     _check(k.dim() == 2 and k.shape[1] == INDEX_HEAD_DIM,
            f"k_idx must be [S, {INDEX_HEAD_DIM}], got {tuple(k.shape)}")
     S = k.shape[0]
+    scale = k_scale.contiguous()
+    _check(tuple(scale.shape) == (S,) and scale.dtype == torch.float32, "k_scale must be [S] float32")
+    return _indexer(q_idx, S, weights, causal_limit, topk, block_table, page_size, return_scores,
+                    flat=(k, scale))
+
+
+def run_indexer_and_topk_paged(q_idx: torch.Tensor, k_cache: torch.Tensor, k_pages: torch.Tensor,
+                               num_positions: int, weights: torch.Tensor,
+                               causal_limit: torch.Tensor, topk: int,
+                               block_table: Optional[torch.Tensor] = None, page_size: int = 64,
+                               return_scores: bool = False):
+    """:func:`run_indexer_and_topk` over a paged fp8 K cache (the format
+    :func:`k_append` writes): position ``s < num_positions`` is token
+    ``s % kps`` of page ``k_pages[s // kps]``, ``kps`` being the cache's page
+    size.  The results equal those of the flat call on the same codes and
+    scales, bit for bit."""
+    cache, kps = _k_cache_view(k_cache)
+    pages = k_pages.contiguous()
+    S = int(num_positions)
+    _check(S >= 0, "num_positions must be >= 0")
+    _check(pages.dtype == torch.int32 and pages.dim() == 1 and pages.numel() * kps >= S,
+           f"k_pages must be int32 [>= {-(-S // kps)}]")
+    return _indexer(q_idx, S, weights, causal_limit, topk, block_table, page_size, return_scores,
+                    paged=(cache, pages, kps))
+
+
+def _indexer(q_idx, S, weights, causal_limit, topk, block_table, page_size, return_scores,
+             flat=None, paged=None):
+    q = _codes(q_idx, "q_idx")
+    _check(q.dim() == 3 and q.shape[2] == INDEX_HEAD_DIM,
+           f"q_idx must be [T, heads, {INDEX_HEAD_DIM}], got {tuple(q.shape)}")
+    T, Hi, _ = q.shape
     _check(Hi in (16, 32, 48, 64), f"index heads must be 16, 32, 48 or 64, got {Hi}")
     dev = q.device
     _check(dev.type == "cuda", "tensors must live on a GPU device")
-    scale = k_scale.contiguous()
     w = weights.contiguous()
     lim = causal_limit.contiguous()
-    _check(tuple(scale.shape) == (S,) and scale.dtype == torch.float32, "k_scale must be [S] float32")
     _check(tuple(w.shape) == (T, Hi) and w.dtype == torch.float32, "weights must be [T, heads] float32")
     _check(tuple(lim.shape) == (T,) and lim.dtype == torch.int32, "causal_limit must be [T] int32")
     _check(int(topk) >= 0, "topk must be >= 0")
-    for name, x in (("k_idx", k), ("k_scale", scale), ("weights", w), ("causal_limit", lim)):
+    held = [x for x in (flat or paged) if isinstance(x, torch.Tensor)]
+    for name, x in [("weights", w), ("causal_limit", lim)] + [("k", x) for x in held]:
         _check(x.device == dev, f"{name} is on {x.device}, expected {dev}")
     bt = None
     bt_stride = 0
@@ -94,7 +121,11 @@ def run_indexer_and_topk(q_idx: torch.Tensor, k_idx: torch.Tensor, k_scale: torc
     ws_bytes = lib.dsa_indexer_workspace_bytes(T, Hi, INDEX_HEAD_DIM, S)
     ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
     a = _lib.IndexerArgs()
-    a.q_idx, a.k_idx, a.k_scale, a.weights = q.data_ptr(), k.data_ptr(), scale.data_ptr(), w.data_ptr()
+    a.q_idx, a.weights = q.data_ptr(), w.data_ptr()
+    if flat is not None:
+        a.k_idx, a.k_scale = flat[0].data_ptr(), flat[1].data_ptr()
+    else:
+        a.k_cache, a.k_pages, a.k_page_size = paged[0].data_ptr(), paged[1].data_ptr(), paged[2]
     a.causal_limit = lim.data_ptr()
     a.num_tokens, a.num_heads, a.head_dim, a.num_positions, a.topk = T, Hi, INDEX_HEAD_DIM, S, int(topk)
     a.block_table = bt.data_ptr() if bt is not None else None
@@ -106,14 +137,72 @@ def run_indexer_and_topk(q_idx: torch.Tensor, k_idx: torch.Tensor, k_scale: torc
     return (out, scores) if return_scores else out
 
 
+K_TOKEN_BYTES = INDEX_HEAD_DIM + 4  # e4m3 codes + fp32 scale per token
+
+
+def new_k_cache(num_pages: int, page_size: int, device) -> torch.Tensor:
+    """An empty paged fp8 indexer K cache ``uint8 [num_pages, page_size * 132]``:
+    per page the ``page_size x 128`` e4m3fn codes, then the ``page_size`` fp32
+    scales."""
+    _check(int(page_size) > 0 and int(page_size) % 4 == 0, "page_size must be a multiple of 4")
+    return torch.zeros((int(num_pages), int(page_size) * K_TOKEN_BYTES), dtype=torch.uint8,
+                       device=device)
+
+
+def _k_cache_view(k_cache: torch.Tensor):
+    _check(k_cache.dtype == torch.uint8 and k_cache.dim() == 2
+           and k_cache.shape[1] % K_TOKEN_BYTES == 0 and k_cache.is_contiguous(),
+           "k_cache must be a contiguous uint8 [pages, page_size * 132] tensor (see new_k_cache)")
+    kps = k_cache.shape[1] // K_TOKEN_BYTES
+    _check(kps % 4 == 0, "the K cache page size must be a multiple of 4")
+    return k_cache, kps
+
+
+def k_append(k: torch.Tensor, slots: torch.Tensor, k_cache: torch.Tensor) -> torch.Tensor:
+    """Quantise bf16 rows ``k [n, 128]`` to e4m3fn with one fp32 scale per row
+    (``max(amax, 1e-4) / 448``) and write them to ``slots [n]`` (slot =
+    page * page_size + offset; negative slots are skipped) of ``k_cache`` in
+    place; returns ``k_cache``."""
+    cache, kps = _k_cache_view(k_cache)
+    _check(k.dtype == torch.bfloat16 and k.dim() == 2 and k.shape[1] == INDEX_HEAD_DIM,
+           f"k must be bfloat16 [n, {INDEX_HEAD_DIM}], got {k.dtype} {tuple(k.shape)}")
+    kk = k if (k.stride(1) == 1 and k.stride(0) % 8 == 0 and k.data_ptr() % 16 == 0) else k.contiguous()
+    sl = slots.contiguous()
+    _check(sl.dtype == torch.int32 and tuple(sl.shape) == (k.shape[0],), "slots must be int32 [n]")
+    _check(kk.device == cache.device == sl.device and cache.device.type == "cuda",
+           "k, slots and k_cache must live on one GPU device")
+    a = _lib.KAppendArgs()
+    a.k, a.k_stride, a.slots, a.num_tokens = kk.data_ptr(), kk.stride(0), sl.data_ptr(), kk.shape[0]
+    a.k_cache, a.num_pages, a.page_size = cache.data_ptr(), cache.shape[0], kps
+    lib = _lib.load()
+    _lib.check("dsa_indexer_k_append",
+               lib.dsa_indexer_k_append(ctypes.byref(a), _stream_handle(cache.device)))
+    return k_cache
+
+
 def run_sparse_attention_pipeline(q_idx, k_idx, k_scale, weights, causal_limit, block_table,
                                   q_nope, q_pe, ckv_cache, kpe_cache, sm_scale, topk: int = 2048,
-                                  page_size: Optional[int] = None):
+                                  page_size: Optional[int] = None,
+                                  k_cache: Optional[torch.Tensor] = None,
+                                  k_pages: Optional[torch.Tensor] = None,
+                                  num_positions: Optional[int] = None):
     """Indexer -> top-k slots -> sparse attention, on one stream, no host sync
     (reference ``kernel.py:184-332``).  ``page_size`` defaults to the cache's.
+    With ``k_cache`` (a paged fp8 K cache, see :func:`k_append`; ``k_idx`` and
+    ``k_scale`` then None) the indexer reads ``num_positions`` positions
+    through ``k_pages``, by default the sequence's 1-D ``block_table``.
     Returns ``(output [T,H,512] bf16, lse [T,H] fp32 base-2, slots [T,topk])``."""
     ps = int(page_size) if page_size is not None else (ckv_cache.shape[1] if ckv_cache.dim() == 3 else 1)
-    slots = run_indexer_and_topk(q_idx, k_idx, k_scale, weights, causal_limit, topk,
-                                 block_table=block_table, page_size=ps)
+    if k_cache is not None:
+        _check(k_idx is None and k_scale is None, "give k_idx/k_scale or k_cache, not both")
+        pages = k_pages if k_pages is not None else block_table
+        _check(pages is not None and pages.dim() == 1,
+               "k_pages (or a 1-D block_table) must map positions to K-cache pages")
+        _check(num_positions is not None, "num_positions is required with k_cache")
+        slots = run_indexer_and_topk_paged(q_idx, k_cache, pages, int(num_positions), weights,
+                                           causal_limit, topk, block_table=block_table, page_size=ps)
+    else:
+        slots = run_indexer_and_topk(q_idx, k_idx, k_scale, weights, causal_limit, topk,
+                                     block_table=block_table, page_size=ps)
     out, lse = kernel(q_nope, q_pe, ckv_cache, kpe_cache, slots, sm_scale)
     return out, lse, slots

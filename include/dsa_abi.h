@@ -23,6 +23,11 @@
  *                         replace the per-call torch.zeros scratch of
  *                         kernel.py:526-528 and indexer_kernel.py:376-378
  *                         with a caller-owned workspace.
+ *   dsa_indexer_k_append  no kernel in the reference: writes the paged fp8
+ *                         indexer K cache that indexer_kernel.py:163-197
+ *                         reads (quantise-on-append).
+ *   dsa_attn_counter_bytes  no counterpart: size of the optional split
+ *                         counters of dsa_attn_fwd.
  */
 #ifndef DSA_ABI_H
 #define DSA_ABI_H
@@ -34,7 +39,7 @@
 extern "C" {
 #endif
 
-#define DSA_ABI_VERSION 2
+#define DSA_ABI_VERSION 3
 
 #define DSA_OK 0
 #define DSA_EINVAL 1      /* bad pointer, size, stride or alignment */
@@ -199,9 +204,46 @@ typedef struct dsa_indexer_args {
   float *scores_out;
   void *workspace;
   size_t workspace_bytes;
+  /* Optional paged fp8 K cache (then k_idx and k_scale are NULL): position
+   * s is token s % k_page_size of page k_pages[s / k_page_size] of k_cache
+   * (layout below); k_page_size a multiple of 4, k_cache 16-byte aligned. */
+  const uint8_t *k_cache;
+  const int32_t *k_pages;
+  int64_t k_page_size;
 } dsa_indexer_args;
 
 int dsa_indexer_topk(const dsa_indexer_args *args, void *stream);
+
+/*
+ * Paged fp8 indexer K cache and its quantise-on-append (the K-cache format on
+ * either side of the indexer; the reference's kernel reads a 129-element
+ * record whose scale is one int8 element, indexer_kernel.py:163-197).  Page
+ * p is k_page_size tokens of DSA_INDEXER_K_TOKEN_BYTES bytes: bytes
+ * [0, 128*page_size) hold the e4m3fn codes of token o at o*128, bytes
+ * [128*page_size, 132*page_size) its fp32 scale at 128*page_size + 4*o (the
+ * codes of a page stay contiguous).  A slot id is page*page_size + offset.
+ *
+ * dsa_indexer_k_append quantises each bf16 row k[i, 0:128] to that format and
+ * writes it to slot slots[i] (negative or out-of-range slots are skipped):
+ *   amax = max_j |k[i,j]| (fp32), scale = fl32(max(amax, 1e-4f) / 448),
+ *   code_j = e4m3fn, rounded to nearest even, of clamp(fl32(k[i,j] / scale),
+ *   -448, 448).
+ * Rows are 16-byte aligned with row stride k_stride elements; page_size a
+ * multiple of 4 and k_cache 16-byte aligned.  Calls with overlapping slots
+ * race like any concurrent writes.
+ */
+#define DSA_INDEXER_K_TOKEN_BYTES 132
+
+typedef struct dsa_k_append_args {
+  const void *k;          /* [num_tokens, 128] bf16 */
+  int64_t k_stride;
+  const int32_t *slots;   /* [num_tokens] */
+  int64_t num_tokens;
+  uint8_t *k_cache;       /* [num_pages, page_size * 132] */
+  int64_t num_pages, page_size;
+} dsa_k_append_args;
+
+int dsa_indexer_k_append(const dsa_k_append_args *args, void *stream);
 
 size_t dsa_indexer_workspace_bytes(int64_t num_tokens, int64_t num_heads, int64_t head_dim,
                                    int64_t num_positions);

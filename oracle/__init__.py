@@ -15,6 +15,10 @@ function names the reference code it restates:
   with the exact rounding order documented in ``dsa_oracle.c``
 * :func:`topk` -- the selection ``indexer_kernel.py:289-343`` intends
   (score desc, ties to the lower index)
+* :func:`e4m3_encode`, :func:`quantize_k`, :func:`pack_k_cache` -- the
+  quantise-on-append into the paged fp8 K cache whose records
+  ``indexer_kernel.py:163-197`` reads (the reference has no quantisation
+  kernel; the formula is the one ``include/dsa_abi.h`` documents)
 """
 from __future__ import annotations
 
@@ -142,3 +146,59 @@ def topk(scores, limit, k: int) -> np.ndarray:
     if rc != 0:
         raise ValueError(f"oracle_topk failed (status {rc})")
     return out
+
+
+def e4m3_encode(y) -> np.ndarray:
+    """float32 -> e4m3fn codes: the nearest finite e4m3fn value (found by
+    search over the 127 non-negative codes, in ascending value order), ties
+    to the even code; the sign bit copied (so -0.0 -> 0x80).  |y| <= 448."""
+    y = np.asarray(y, dtype=np.float32)
+    mag = np.abs(y)
+    vals = e4m3_decode(np.arange(0x7f))            # codes 0x00..0x7e, ascending
+    hi = np.clip(np.searchsorted(vals, mag, side="left"), 0, len(vals) - 1)
+    lo = np.clip(hi - 1, 0, len(vals) - 1)
+    d_lo = np.abs(mag - vals[lo])
+    d_hi = np.abs(vals[hi] - mag)
+    pick = np.where(d_lo < d_hi, lo, np.where(d_hi < d_lo, hi, np.where(lo % 2 == 0, lo, hi)))
+    return (pick.astype(np.uint8) | np.where(np.signbit(y), 0x80, 0).astype(np.uint8)).astype(np.uint8)
+
+
+def quantize_k(k) -> tuple:
+    """Quantise rows ``k [n, 128]`` (float32 values, e.g. bf16 inputs) with one
+    fp32 scale per row: ``scale = fl32(fmax(amax, 1e-4) / 448)``, ``code =
+    e4m3_encode(fmin(fmax(fl32(k / scale), -448), 448))`` (fmax/fmin ignore
+    NaN).  Returns ``(codes uint8 [n, 128], scale float32 [n])``."""
+    k = np.asarray(k, dtype=np.float32)
+    amax = np.fmax.reduce(np.abs(k), axis=1).astype(np.float32)
+    scale = (np.fmax(amax, np.float32(1e-4)) / np.float32(448.0)).astype(np.float32)
+    y = (k / scale[:, None]).astype(np.float32)
+    y = np.fmin(np.fmax(y, np.float32(-448.0)), np.float32(448.0)).astype(np.float32)
+    return e4m3_encode(y), scale
+
+
+def pack_k_cache(cache, codes, scale, slots, page_size: int) -> np.ndarray:
+    """Write rows into a paged fp8 K cache ``uint8 [pages, page_size * 132]``
+    (a copy of ``cache`` is returned): per page the ``page_size x 128`` codes,
+    then the ``page_size`` fp32 scales; slot = page * page_size + offset;
+    negative or out-of-range slots are skipped."""
+    out = np.array(cache, dtype=np.uint8, copy=True)
+    pages = out.shape[0]
+    sc_bytes = np.asarray(scale, dtype=np.float32).view(np.uint8).reshape(-1, 4)
+    for i, sl in enumerate(np.asarray(slots).tolist()):
+        if sl < 0 or sl >= pages * page_size:
+            continue
+        pg, off = divmod(sl, page_size)
+        out[pg, off * 128:(off + 1) * 128] = codes[i]
+        base = page_size * 128 + off * 4
+        out[pg, base:base + 4] = sc_bytes[i]
+    return out
+
+
+def unpack_k_cache(cache, page_size: int, slots) -> tuple:
+    """Codes ``[n, 128]`` and scales ``[n]`` of the given slots of a paged cache."""
+    cache = np.asarray(cache, dtype=np.uint8)
+    slots = np.asarray(slots, dtype=np.int64)
+    pg, off = slots // page_size, slots % page_size
+    rows = cache[pg[:, None], off[:, None] * 128 + np.arange(128)[None, :]]
+    sb = cache[pg[:, None], page_size * 128 + off[:, None] * 4 + np.arange(4)[None, :]]
+    return rows, np.ascontiguousarray(sb).view(np.float32).reshape(-1)

@@ -37,9 +37,10 @@ def test_header_functions_are_exported():
 def test_abi_version_and_struct_layout(tmp_path):
     """The ctypes mirrors match the C structs field by field (gcc offsetof)."""
     lib = _lib.load()
-    assert lib.dsa_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.dsa_abi_version() == _lib.ABI_VERSION == 3
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "dsa_abi.h"', 'int main(void){']
-    for cname, cls in (("dsa_attn_args", _lib.AttnArgs), ("dsa_indexer_args", _lib.IndexerArgs)):
+    for cname, cls in (("dsa_attn_args", _lib.AttnArgs), ("dsa_indexer_args", _lib.IndexerArgs),
+                        ("dsa_k_append_args", _lib.KAppendArgs)):
         lines.append(f'printf("{cname} %zu\\n", sizeof({cname}));')
         for f, _ in cls._fields_:
             lines.append(f'printf("{cname}.{f} %zu\\n", offsetof({cname}, {f}));')
@@ -49,7 +50,8 @@ def test_abi_version_and_struct_layout(tmp_path):
     exe = tmp_path / "layout"
     subprocess.check_call(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)])
     got = dict(l.split() for l in subprocess.check_output([str(exe)], text=True).splitlines())
-    for cname, cls in (("dsa_attn_args", _lib.AttnArgs), ("dsa_indexer_args", _lib.IndexerArgs)):
+    for cname, cls in (("dsa_attn_args", _lib.AttnArgs), ("dsa_indexer_args", _lib.IndexerArgs),
+                        ("dsa_k_append_args", _lib.KAppendArgs)):
         assert int(got[cname]) == ctypes.sizeof(cls)
         for f, _ in cls._fields_:
             assert int(got[f"{cname}.{f}"]) == getattr(cls, f).offset, f
@@ -188,6 +190,13 @@ def _idx_args(**kw):
     (dict(k_idx=0x2008), _lib.DSA_EINVAL, "misaligned"),
     (dict(block_table=0x7000, page_size=0), _lib.DSA_EINVAL, "block_table"),
     (dict(workspace_bytes=1024), _lib.DSA_EWORKSPACE, "workspace"),
+    (dict(k_cache=0x9000, k_pages=0xa000, k_page_size=64), _lib.DSA_EINVAL, "not both"),
+    (dict(k_idx=None, k_scale=None, k_cache=0x9000, k_pages=None, k_page_size=64),
+     _lib.DSA_EINVAL, "k_pages"),
+    (dict(k_idx=None, k_scale=None, k_cache=0x9000, k_pages=0xa000, k_page_size=62),
+     _lib.DSA_EINVAL, "multiple of 4"),
+    (dict(k_idx=None, k_scale=None, k_cache=0x9008, k_pages=0xa000, k_page_size=64),
+     _lib.DSA_EINVAL, "misaligned"),
 ])
 def test_indexer_host_validation(kw, code, needle):
     lib = _lib.load()
@@ -198,15 +207,41 @@ def test_indexer_host_validation(kw, code, needle):
 def test_indexer_workspace_and_empty_call():
     lib = _lib.load()
     # k operand chunks (3 pieces x 2 k-steps x 1 KB per 16 positions) + block
-    # maxima, q operand chunks (per token and 16 heads) + their maxima, fp32
-    # scores; each region 256-aligned
+    # maxima, q operand chunks (per token and 16 heads) + their maxima, the
+    # per-position scales of a paged K cache, fp32 scores; each region
+    # 256-aligned
     def up(x):
         return (x + 255) // 256 * 256
 
     kb, qb = 32768 // 16, 64 * 64 // 16
-    want = up(kb * 6144) + up(kb * 4) + up(qb * 6144) + up(qb * 4) + up(64 * 32768 * 4)
+    want = (up(kb * 6144) + up(kb * 4) + up(qb * 6144) + up(qb * 4) + up(32768 * 4)
+            + up(64 * 32768 * 4))
     assert lib.dsa_indexer_workspace_bytes(64, 64, 128, 32768) == want
     kb, qb = (1000 + 15) // 16, 3 * 48 // 16
-    want = up(kb * 6144) + up(kb * 4) + up(qb * 6144) + up(qb * 4) + up(3 * 1000 * 4)
+    want = up(kb * 6144) + up(kb * 4) + up(qb * 6144) + up(qb * 4) + up(1000 * 4) + up(3 * 1000 * 4)
     assert lib.dsa_indexer_workspace_bytes(3, 48, 128, 1000) == want
     assert lib.dsa_indexer_topk(ctypes.byref(_idx_args(num_tokens=0, q_idx=None)), None) == 0
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(page_size=6), _lib.DSA_EINVAL, "multiple of 4"),
+    (dict(num_tokens=-1), _lib.DSA_EINVAL, "num_tokens"),
+    (dict(k=None), _lib.DSA_EINVAL, "NULL"),
+    (dict(k=0x1008), _lib.DSA_EINVAL, "aligned"),
+    (dict(k_stride=100), _lib.DSA_EINVAL, "aligned"),
+    (dict(k_cache=0x3004), _lib.DSA_EINVAL, "aligned"),
+])
+def test_k_append_host_validation(kw, code, needle):
+    lib = _lib.load()
+    a = _lib.KAppendArgs()
+    base = dict(k=0x1000, k_stride=128, slots=0x2000, num_tokens=16, k_cache=0x3000,
+                num_pages=8, page_size=64)
+    base.update(kw)
+    for k, v in base.items():
+        setattr(a, k, v)
+    rc = lib.dsa_indexer_k_append(ctypes.byref(a), None)
+    assert rc == code and needle in lib.dsa_last_error().decode()
+    a.num_tokens = 0
+    a.k = 0x1000
+    a.k_stride, a.page_size, a.k_cache = 128, 64, 0x3000
+    assert lib.dsa_indexer_k_append(ctypes.byref(a), None) == 0   # nothing to do

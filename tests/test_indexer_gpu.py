@@ -218,3 +218,99 @@ def test_graph_replays_match_eager():
         assert torch.equal(out, eager)
         run_indexer_and_topk(*args, 100)   # eager work between replays
         torch.cuda.synchronize()
+
+
+# ---- paged fp8 K cache ---------------------------------------------------
+
+def _bf16_rows(g, n):
+    """bf16 rows with a spread of magnitudes, a zero row, -0.0 and tiny rows."""
+    k = torch.randn(n, 128, generator=g) * torch.exp2(torch.randint(-12, 12, (n, 1), generator=g).float())
+    k[0] = 0.0
+    k[1, 7] = -0.0
+    k[2] *= 1e-30                                   # amax below the 1e-4 floor
+    k[3, :64] = 3e4                                  # large, many equal magnitudes
+    return k.to(torch.bfloat16)
+
+
+def test_k_append_matches_oracle_bit_exact():
+    """Quantise-on-append writes exactly the oracle's codes and fp32 scales to
+    each slot's place in the page layout and leaves every other byte alone
+    (negative and out-of-range slots are skipped)."""
+    from dsa_amd import k_append
+    g = torch.Generator().manual_seed(41)
+    ps, pages, n = 64, 40, 1500
+    k = _bf16_rows(g, n)
+    slots = torch.randperm(pages * ps, generator=g)[:n].to(torch.int32)
+    slots[10] = -1
+    slots[11] = pages * ps + 5
+    base = torch.randint(0, 256, (pages, ps * 132), generator=g, dtype=torch.uint8)
+    cache = base.to(DEV)
+    print("k_append n=1500 pages=40 ps=64", flush=True)
+    k_append(k.to(DEV), slots.to(DEV), cache)
+    torch.cuda.synchronize()
+    codes, scale = oracle.quantize_k(k.float().numpy())
+    want = oracle.pack_k_cache(base.numpy(), codes, scale, slots.numpy(), ps)
+    got = cache.cpu().numpy()
+    bad = np.flatnonzero(got != want)
+    assert bad.size == 0, f"{bad.size} bytes differ, first at {np.unravel_index(bad[0], got.shape)}"
+    # strided rows (a view of a wider tensor) give the same bytes
+    wide = torch.zeros(n, 256, dtype=torch.bfloat16)
+    wide[:, 64:192] = k
+    cache2 = base.to(DEV)
+    k_append(wide.to(DEV)[:, 64:192], slots.to(DEV), cache2)
+    torch.cuda.synchronize()
+    assert torch.equal(cache2.cpu(), cache.cpu())
+
+
+def test_paged_indexer_equals_flat_bit_for_bit():
+    """The indexer over a paged K cache (pages in a random order, appended by
+    k_append) returns the same scores and slots as the flat call over the
+    same codes and scales."""
+    from dsa_amd import k_append, new_k_cache, run_indexer_and_topk_paged
+    g = torch.Generator().manual_seed(42)
+    T, Hi, S, ps, topk = 12, 64, 6000, 64, 512
+    d = workloads.indexer_inputs(T=T, Hi=Hi, S=S, seed=43)
+    k = torch.randn(S, 128, generator=g).to(torch.bfloat16)
+    n_pages = -(-S // ps) + 3
+    page_of = torch.randperm(n_pages, generator=g)[:-(-S // ps)].to(torch.int32)  # position page -> cache page
+    pos = torch.arange(S)
+    slots = (page_of[pos // ps] * ps + pos % ps).to(torch.int32)
+    cache = new_k_cache(n_pages, ps, DEV)
+    k_append(k.to(DEV), slots.to(DEV), cache)
+    codes, scale = oracle.quantize_k(k.float().numpy())
+    flat = dict(d, k_idx=torch.from_numpy(codes), k_scale=torch.from_numpy(scale))
+    ref_idx, ref_sc = _gpu_indexer(flat, topk)
+    gd = workloads.to_device(d, DEV)
+    out, sc = run_indexer_and_topk_paged(gd["q_idx"], cache, page_of.to(DEV), S, gd["weights"],
+                                         gd["causal_limit"], topk, return_scores=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(sc.cpu().numpy().view(np.uint32), ref_sc.view(np.uint32))
+    assert np.array_equal(out.cpu().numpy(), ref_idx)
+    ora_idx, ora_sc = _oracle(flat, topk)
+    _assert_same(ref_idx, ref_sc, ora_idx, ora_sc, "flat over the quantised K")
+
+
+def test_pipeline_over_paged_k_cache_equals_flat():
+    """cfg5's indexer K packed into a paged cache that shares the attention's
+    block table: the pipeline gives the same slots, output and lse as over the
+    flat K."""
+    d = workloads.cfg5()
+    g = workloads.to_device(d, DEV)
+    ps = 64
+    S = d["k_idx"].shape[0]
+    bt = d["block_table"]
+    assert bt.dim() == 1
+    pos = torch.arange(S)
+    slots = (bt[pos // ps].long() * ps + pos % ps).numpy()
+    base = np.zeros((bt.numel(), ps * 132), np.uint8)
+    cache = oracle.pack_k_cache(base, d["k_idx"].view(torch.uint8).numpy(), d["k_scale"].numpy(),
+                                slots, ps)
+    args = (g["q_nope"], g["q_pe"], g["ckv_cache"], g["kpe_cache"], d["sm_scale"])
+    flat = run_sparse_attention_pipeline(g["q_idx"], g["k_idx"], g["k_scale"], g["weights"],
+                                         g["causal_limit"], g["block_table"], *args, topk=2048)
+    paged = run_sparse_attention_pipeline(g["q_idx"], None, None, g["weights"], g["causal_limit"],
+                                          g["block_table"], *args, topk=2048,
+                                          k_cache=torch.from_numpy(cache).to(DEV), num_positions=S)
+    torch.cuda.synchronize()
+    for a, b in zip(flat, paged):
+        assert torch.equal(a, b)

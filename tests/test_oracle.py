@@ -308,3 +308,58 @@ def test_topk_pads_short_rows():
     sc = np.array([[3.0, 1.0, 2.0, 5.0]], np.float32)
     got = oracle.topk(sc, np.array([2]), 5)
     assert got.tolist() == [[0, 2, 1, -1, -1]]
+
+
+# ---- quantise-on-append into the paged fp8 K cache ----------------------
+
+def test_e4m3_encode_matches_torch_cast_including_ties():
+    rng = np.random.default_rng(0)
+    vals = oracle.e4m3_decode(np.arange(0x7f))
+    mids = (vals[:-1] + vals[1:]) / 2                 # every tie between neighbours
+    y = np.concatenate([rng.uniform(-448, 448, 20000), rng.uniform(-0.02, 0.02, 20000), vals,
+                        -vals, mids, -mids,
+                        [0.0, -0.0, 448.0, -448.0, 2.0 ** -10, 3 * 2.0 ** -11]]).astype(np.float32)
+    want = torch.from_numpy(y).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(oracle.e4m3_encode(y), want)
+
+
+def test_quantize_k_closed_forms():
+    rng = np.random.default_rng(1)
+    k = rng.standard_normal((6, 128)).astype(np.float32)
+    k[1] = 0.0                                         # zero row: floor scale, zero codes
+    k[2, 5] = -0.0
+    k[3] *= 1e-7                                       # amax below the 1e-4 floor
+    codes, scale = oracle.quantize_k(k)
+    assert scale.dtype == np.float32 and codes.dtype == np.uint8
+    assert scale[1] == np.float32(np.float32(1e-4) / np.float32(448.0)) and not codes[1].any()
+    for r in (0, 2, 4, 5):                             # the largest magnitude encodes to +-448
+        j = int(np.argmax(np.abs(k[r])))
+        assert codes[r, j] == (0xfe if k[r, j] < 0 else 0x7e)
+    assert np.abs(oracle.e4m3_decode(codes[3])).max() < 448.0
+    # scaling a row by a power of two scales its scale exactly and keeps its codes
+    c2, s2 = oracle.quantize_k(k[[0, 4]] * np.float32(64.0))
+    assert np.array_equal(c2, codes[[0, 4]]) and np.array_equal(s2, scale[[0, 4]] * np.float32(64.0))
+    # decoded values are within half an e4m3 step (relative 2^-4) of k / scale
+    dec = oracle.e4m3_decode(codes) * scale[:, None]
+    err = np.abs(dec - k)
+    assert np.all(err <= np.abs(k) * 2.0 ** -4 + scale[:, None] * 2.0 ** -10 + 1e-30)
+
+
+def test_k_cache_pack_unpack_roundtrip():
+    rng = np.random.default_rng(2)
+    ps, pages = 8, 5
+    codes = rng.integers(0, 256, (12, 128), dtype=np.uint8)
+    scale = rng.uniform(0.001, 2, 12).astype(np.float32)
+    slots = rng.permutation(ps * pages)[:12]
+    slots[3] = -1                                       # skipped
+    base = rng.integers(0, 256, (pages, ps * 132), dtype=np.uint8)
+    cache = oracle.pack_k_cache(base, codes, scale, slots, ps)
+    keep = slots >= 0
+    c, s = oracle.unpack_k_cache(cache, ps, slots[keep])
+    assert np.array_equal(c, codes[keep]) and np.array_equal(s, scale[keep])
+    touched = np.zeros_like(base, dtype=bool)
+    for sl in slots[keep]:
+        pg, off = divmod(int(sl), ps)
+        touched[pg, off * 128:(off + 1) * 128] = True
+        touched[pg, ps * 128 + off * 4:ps * 128 + off * 4 + 4] = True
+    assert np.array_equal(cache[~touched], base[~touched])
