@@ -34,6 +34,9 @@
 //                          operands in lane order (one 1 KB chunk per 16 rows,
 //                          piece and 64-wide k-step), plus the largest |x|
 //                          of every 16-row block.
+//                          With a paged K cache it reads each position's
+//                          codes through the page map and copies its fp32
+//                          scale to a contiguous workspace array.
 //   dsa_idx_score_kernel   one wave per query token, up to 8 tokens per
 //                          workgroup sharing a range of positions.  The
 //                          token's q pieces stay in registers (A operands,
@@ -41,18 +44,25 @@
 //                          one coalesced 1 KB load per operand (B, positions
 //                          as N).  No LDS and no barriers.
 //   dsa_idx_topk_kernel    one workgroup per row, the row in registers
-//                          (loaded coalesced, 1024-strided): 4-pass radix
-//                          select (8 bits per pass, histograms replicated 32
-//                          ways so equal digits do not collide in one LDS
-//                          bank) of the k-th largest order key; the keys then
-//                          move through LDS so that each thread owns a
-//                          contiguous run of positions, and one packed scan
-//                          places every larger score and the lowest positions
-//                          among the ties in ascending position order
-//                          (reference intent: indexer_kernel.py:289-343,
-//                          strict '>' keeps the earlier index).
-//   dsa_idx_topk_stream_kernel  the same selection re-reading the row from
-//                          memory, for rows longer than 32768 positions.
+//                          (loaded coalesced, 1024-strided, through one
+//                          buffer descriptor): two radix passes (8 bits each,
+//                          histograms replicated 32 ways so equal digits do
+//                          not collide in one LDS bank) find the 16-bit bin
+//                          of the k-th largest order key; keys above it are
+//                          taken and the bin's few survivors are ranked
+//                          exactly (key, then lower position first), else
+//                          two more passes pin the k-th key and its ties go
+//                          lowest positions first (reference intent:
+//                          indexer_kernel.py:289-343, strict '>' keeps the
+//                          earlier index).  The selection is a position
+//                          bitmap built from ballots; one scan turns it into
+//                          ranks in ascending position order.
+//   dsa_idx_topk_stream_kernel  the four-pass selection re-reading the row
+//                          from memory, for rows longer than 32768 positions.
+//   dsa_k_append_kernel    quantise-on-append into the paged fp8 K cache:
+//                          one wave per token (per-token fp32 scale from the
+//                          row's largest magnitude, e4m3 round to nearest
+//                          even).
 #include <algorithm>
 
 #include "../../include/dsa_abi.h"
