@@ -306,10 +306,10 @@ IndexerWorkspace indexer_workspace_layout(int64_t T, int64_t Hi, int64_t S, bool
   w.k_max = off;
   off += up256(kblocks * 4);
   w.q_pieces = off;
-  off += up256(qblocks * 3 * 2 * 1024);
+  off += up256(qblocks * 4 * 2 * 1024);
   w.q_max = off;
   off += up256(qblocks * 4);
-  w.k_scale = off;
+  w.k_cs = off;
   off += up256((size_t)S * 4);
   w.scores = off;
   if (own_scores) off += up256((size_t)T * (size_t)S * 4);
@@ -381,12 +381,11 @@ int dsa_indexer_topk(const dsa_indexer_args *a, void *stream) {
   p.k_max = reinterpret_cast<int32_t *>(ws + lay.k_max);
   p.q_pieces = reinterpret_cast<int8_t *>(ws + lay.q_pieces);
   p.q_max = reinterpret_cast<int32_t *>(ws + lay.q_max);
+  p.k_cs = reinterpret_cast<float *>(ws + lay.k_cs);
   if (paged) {
     p.k_cache = a->k_cache;
     p.k_pages = a->k_pages;
     p.k_page_size = (int32_t)a->k_page_size;
-    p.k_scale_ws = reinterpret_cast<float *>(ws + lay.k_scale);
-    p.k_scale = p.k_scale_ws;
   }
   p.scores = a->scores_out ? a->scores_out : reinterpret_cast<float *>(ws + lay.scores);
   const hipError_t e = dsa::launch_indexer(p, static_cast<hipStream_t>(stream));

@@ -33,16 +33,20 @@
 //   dsa_idx_prep_kernel    q and k codes -> piece planes laid out as MFMA
 //                          operands in lane order (one 1 KB chunk per 16 rows,
 //                          piece and 64-wide k-step), plus the largest |x|
-//                          of every 16-row block.
-//                          With a paged K cache it reads each position's
-//                          codes through the page map and copies its fp32
-//                          scale to a contiguous workspace array.
+//                          of every 16-row block, and c_s of every position
+//                          in a contiguous workspace array.  With a paged K
+//                          cache it reads each position's codes and scale
+//                          through the page map.
 //   dsa_idx_score_kernel   one wave per query token, up to 8 tokens per
 //                          workgroup sharing a range of positions.  The
 //                          token's q pieces stay in registers (A operands,
 //                          heads as M); each 16-position block's k pieces are
 //                          one coalesced 1 KB load per operand (B, positions
-//                          as N).  No LDS and no barriers.
+//                          as N).  No LDS and no barriers.  When every block
+//                          of a wave's range takes the two-piece int32 path
+//                          the loop is software-pipelined: a head block's
+//                          MFMAs are issued beside the previous head block's
+//                          epilogue.
 //   dsa_idx_topk_kernel    one workgroup per row, the row in registers
 //                          (loaded coalesced, 1024-strided, through one
 //                          buffer descriptor): two radix passes (8 bits each,
@@ -76,7 +80,8 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 constexpr int kIdxDim = 128;
 constexpr int kKTokenBytes = kIdxDim + 4;  // paged K cache: codes + fp32 scale per token
 constexpr int kChunk = 1024;              // one MFMA operand: 64 lanes x 16 bytes
-constexpr int kBlockBytes = 3 * 2 * kChunk;
+constexpr int kBlockBytes = 3 * 2 * kChunk;  // k block: 3 planes x 2 k-steps
+constexpr int kQBlockBytes = 4 * 2 * kChunk; // q head block: 4 planes x 2 k-steps
 constexpr int kPrepThreads = 256;         // two 16-row blocks x 8 segments of 16 bytes
 constexpr int kScoreWaves = 8;            // tokens per score workgroup
 constexpr int kTargetScoreWaves = 2048;   // two waves per SIMD on 256 CUs
@@ -86,6 +91,7 @@ constexpr int kMaxRegEpt = 32;            // register top-k up to 1024 * 32 posi
 constexpr int kHistCopies = 32;
 constexpr int kHistPitch = 257;           // copy c of bin j at c*257 + j: bank (c + j) % 64
 constexpr int kTwoPieceLimit = 1 << 14;
+constexpr int kBufferFlags = 0x00020000;  // raw buffer descriptor: 32-bit data format
 
 // e4m3fn code -> x = value * 2^9 (integer), NaN codes -> 0.
 __device__ __forceinline__ int e4m3_x(uint32_t c) {
@@ -95,7 +101,9 @@ __device__ __forceinline__ int e4m3_x(uint32_t c) {
   return (c & 0x80) ? -x : x;
 }
 
-// Signed 7-bit piece `pc` of x (sign-magnitude split), as a byte.
+// Signed 7-bit piece `pc` of x (sign-magnitude split), as a byte.  The
+// pieces of one value share its sign, so for |x| < 2^14 the difference
+// p0 - p1 of its two pieces lies in [-127, 127] as well.
 __device__ __forceinline__ uint32_t piece_byte(int x, int pc) {
   const int mag = x < 0 ? -x : x;
   const int v = (mag >> (7 * pc)) & 127;
@@ -121,11 +129,14 @@ __device__ __forceinline__ i32x4 mfma(i32x4 a, i32x4 b, i32x4 c) {
 // output rows a lane receives (rows 4g'..4g'+3) are consecutive heads of the
 // lane's head group g'.
 __global__ __launch_bounds__(kPrepThreads) void dsa_idx_prep_kernel(IndexerParams p) {
-  __shared__ uint32_t lut[256];  // code -> signed piece bytes p0 | p1 << 8 | p2 << 16
+  // code -> signed bytes p0 | p1 << 8 | p2 << 16 | (p0 - p1) << 24
+  __shared__ uint32_t lut[256];
   __shared__ uint32_t s_max[2];  // largest magnitude code (code & 0x7f) of each row block
   {
     const int x = e4m3_x(threadIdx.x);
-    lut[threadIdx.x] = piece_byte(x, 0) | (piece_byte(x, 1) << 8) | (piece_byte(x, 2) << 16);
+    const uint32_t b0 = piece_byte(x, 0), b1 = piece_byte(x, 1);
+    const uint32_t d = (uint32_t)((int)(int8_t)b0 - (int)(int8_t)b1) & 0xffu;
+    lut[threadIdx.x] = b0 | (b1 << 8) | (piece_byte(x, 2) << 16) | (d << 24);
   }
   if (threadIdx.x < 2) s_max[threadIdx.x] = 0;
   const int nkb = (p.S + 15) >> 4, nqb = p.Hi >> 4;
@@ -146,9 +157,10 @@ __global__ __launch_bounds__(kPrepThreads) void dsa_idx_prep_kernel(IndexerParam
           const int pg = p.k_pages[s / p.k_page_size], off = s % p.k_page_size;
           const uint8_t *page = p.k_cache + (int64_t)pg * p.k_page_size * kKTokenBytes;
           raw = *(const uint4 *)(page + off * kIdxDim + seg * 16);
-          if (seg == 0) p.k_scale_ws[s] = *(const float *)(page + p.k_page_size * kIdxDim + off * 4);
+          if (seg == 0) p.k_cs[s] = *(const float *)(page + p.k_page_size * kIdxDim + off * 4) * 0x1p-18f;
         } else {
           raw = *(const uint4 *)(p.k + (int64_t)s * kIdxDim + seg * 16);
+          if (seg == 0) p.k_cs[s] = p.k_scale[s] * 0x1p-18f;
         }
       }
     } else {
@@ -171,34 +183,48 @@ __global__ __launch_bounds__(kPrepThreads) void dsa_idx_prep_kernel(IndexerParam
   const uint32_t top = s_max[local];
   const int bmax = top == 0x7f ? (15 << 14) : e4m3_x(top);
 
+  // Planes (slot <- LUT byte).  k block: p0, p1, then p2 if the block holds
+  // a value of magnitude >= 32, else p0 - p1 (slot 2 is read as p2 only for
+  // such blocks).  q head block: p0, p1, p2, and in slot 3 p1 - p0 when every
+  // value of the 16 heads is below 32.
+  const bool two = bmax < kTwoPieceLimit;
   int8_t *dst;
-  int npieces;
   const int ks = seg >> 2, g = seg & 3;
   if (is_k) {
     dst = p.k_pieces + (int64_t)rb * kBlockBytes + ks * kChunk + (16 * g + r) * 16;
-    npieces = bmax >= kTwoPieceLimit ? 3 : 2;  // the third plane is read only then
     if (r == 0 && seg == 0) p.k_max[rb] = bmax;
   } else {
     const int quarter = p.Hi >> 2;
     const int gq = h / quarter, within = h % quarter;
     const int hb = within >> 2, row = 4 * gq + (within & 3);
-    dst = p.q_pieces + ((int64_t)t * nqb + hb) * kBlockBytes + ks * kChunk + (16 * g + row) * 16;
-    npieces = 3;
+    dst = p.q_pieces + ((int64_t)t * nqb + hb) * kQBlockBytes + ks * kChunk + (16 * g + row) * 16;
     if (r == 0 && seg == 0) p.q_max[rb - nkb] = bmax;
   }
   uint32_t v[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) v[i] = lut[(w[i >> 2] >> (8 * (i & 3))) & 0xffu];
-  for (int pc = 0; pc < npieces; ++pc) {
+  auto put = [&](int slot, int byte, bool negate) {
     uint32_t o[4];
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
       uint32_t packed = 0;
 #pragma unroll
-      for (int b = 0; b < 4; ++b) packed |= ((v[4 * d + b] >> (8 * pc)) & 0xffu) << (8 * b);
+      for (int b = 0; b < 4; ++b) {
+        uint32_t x = (v[4 * d + b] >> (8 * byte)) & 0xffu;
+        if (negate) x = (0u - x) & 0xffu;
+        packed |= x << (8 * b);
+      }
       o[d] = packed;
     }
-    *(uint4 *)(dst + pc * 2 * kChunk) = make_uint4(o[0], o[1], o[2], o[3]);
+    *(uint4 *)(dst + slot * 2 * kChunk) = make_uint4(o[0], o[1], o[2], o[3]);
+  };
+  put(0, 0, false);
+  put(1, 1, false);
+  if (is_k) {
+    put(2, two ? 3 : 2, false);
+  } else {
+    put(2, 2, false);
+    if (two) put(3, 3, true);
   }
 }
 
@@ -231,14 +257,14 @@ __device__ __forceinline__ void score_range(const IndexerParams &p, int t, int b
 
   // A operands of this token: [head block][piece][k-step]
   i32x4 qa[NHB][NQP][2];
-  const int8_t *qsrc = p.q_pieces + (int64_t)t * NHB * kBlockBytes + lane * 16;
+  const int8_t *qsrc = p.q_pieces + (int64_t)t * NHB * kQBlockBytes + lane * 16;
 #pragma unroll
   for (int hb = 0; hb < NHB; ++hb)
 #pragma unroll
     for (int pc = 0; pc < NQP; ++pc)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        qa[hb][pc][ks] = load_chunk(qsrc + hb * kBlockBytes + (pc * 2 + ks) * kChunk);
+        qa[hb][pc][ks] = load_chunk(qsrc + hb * kQBlockBytes + (pc * 2 + ks) * kChunk);
   // weights of the lane's rows: heads g*Hi/4 + 4*hb + i
   float wl[NHB][4];
   const float *wsrc = p.w + (int64_t)t * p.Hi + g * (p.Hi >> 2);
@@ -262,14 +288,14 @@ __device__ __forceinline__ void score_range(const IndexerParams &p, int t, int b
     for (int pc = 0; pc < 2; ++pc)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) kb.k[pc][ks] = load_chunk(src + (pc * 2 + ks) * kChunk);
-    kb.cs = p.k_scale[min(b * 16 + col, p.S - 1)];  // scaled by 2^-18 where it is used
+    kb.cs = p.k_cs[min(b * 16 + col, p.S - 1)];
     kb.kmax = p.k_max[b];
   };
 
   // the lane's group sum for its position -> the score, stored by lanes 0..15
   auto finish = [&](float G, float cs, int s) {
     const float total = sum_lane_groups(G);
-    const float score = total * (cs * 0x1p-18f);
+    const float score = total * cs;
     if (g == 0 && s >= 0 && s < p.S) srow[s] = (s > lim) ? -INFINITY : score;
   };
   // int32 combine of one head block's products into the lane's group sum:
@@ -383,6 +409,237 @@ __device__ __forceinline__ void score_range(const IndexerParams &p, int t, int b
   }
 }
 
+// Instruction groups for the scheduler (__builtin_amdgcn_sched_group_barrier
+// masks: 0x002 VALU, 0x008 MFMA, 0x020 vector memory read, 0x040 write): NM
+// MFMAs, each followed by NV VALU instructions.
+template <int NM, int NV>
+__device__ __forceinline__ void mfma_valu_groups() {
+#pragma unroll
+  for (int i = 0; i < NM; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);
+  }
+}
+
+// Scores of token t over the blocks [b0, b1) when every block of the range
+// takes the two-piece int32 path, for NHB >= 2: the same exact D and the same
+// rounding order as score_range, from three piece products instead of four.
+//
+// With the pieces of every value below 2^14 in [0, 127] and of one sign,
+// (q1 - q0) and (k0 - k1) fit int8 (the prep kernel writes them as planes).
+// With P00 = q0.k0, P11 = q1.k1 and the cross term X = q0.k1 + q1.k0,
+// (q1 - q0).(k0 - k1) = X - P00 - P11, so the chain
+//   C3 = P00 + (q1 - q0).(k0 - k1) = X - P11
+// gives D = P00 + 2^7 X + 2^14 P11 = ((C3 + 129 P11) << 7) + P00:
+// six MFMAs per head block (C3's chain starts from P00's result) and two
+// integer instructions per element (v_mad_i32_i24: |P11| < 2^23; the
+// arithmetic is modulo 2^32 and D itself fits int32).  The int8 MFMA path
+// is bound by the chip's power limit, not by issue: fewer MFMAs are faster.
+//
+// Software-pipelined over the range's head blocks j = (b - b0) * NHB + hb:
+// the six MFMAs of head block j are issued between the epilogue
+// instructions of head block j - 2, whose accumulators are complete by then.
+// The loop is unrolled by six blocks, so the three accumulator sets (j mod
+// 3), the three operand buffers (block mod 3, fetched two blocks ahead), the
+// group sums G[block mod 2] and the pair scales all have static indices.  A
+// pair of blocks shares one reduction over the four lane groups (a
+// permlane16 swap of the two blocks' sums, a permlane32 swap, two adds: lane
+// groups 0 and 1 end with blocks q and q + 1), one scale load and one store.
+//
+// Loads and stores go through buffer descriptors with scalar block offsets;
+// scale loads and score stores carry the position in the per-lane offset,
+// which the descriptor's bound checks (positions past S read 0 and are not
+// stored; an offset of 2^31 is past every bound).  No per-block bound is
+// loaded: a wave-uniform loaded value is moved to a scalar register right
+// after its load, a wait that would tie each prefetch to its own step.
+template <int NHB>
+__device__ __forceinline__ void score_range_fast(const IndexerParams &p, int t, int b0, int b1) {
+#pragma clang fp contract(off)
+  static_assert(NHB >= 2, "the epilogue runs two head blocks behind");
+  const int lane = threadIdx.x & 63;
+  const int col = lane & 15, g = lane >> 4;
+  const int lim = p.limit[t];
+  const int nkb = (p.S + 15) >> 4;
+  const auto krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(p.k_pieces), 0,
+                                                     nkb * kBlockBytes, kBufferFlags);
+  const auto srs = __builtin_amdgcn_make_buffer_rsrc(p.k_cs, 0, p.S * 4, kBufferFlags);
+  const auto ors = __builtin_amdgcn_make_buffer_rsrc(p.scores + (int64_t)t * p.S, 0, p.S * 4,
+                                                     kBufferFlags);
+  constexpr uint32_t kDropped = 0x80000000u;  // S * 4 < 2^31
+  const uint32_t pair4 = (uint32_t)((g & 1) * 16 + col) * 4;  // lane's position in a pair, bytes
+  uint32_t sh7;
+  asm volatile("s_mov_b32 %0, 7" : "=s"(sh7));
+
+  // blocks [b0, bend) hold a position at or below the causal limit; every
+  // position of the blocks before bend - 1 is below it
+  const int bend = min(b1, max(b0, (lim >> 4) + 1));
+  for (int b = bend; b < b1; ++b)
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(-INFINITY), ors,
+                                          g == 0 ? col * 4 + b * 64 : kDropped, 0, 0);
+  if (bend == b0) return;
+
+  // A operands [hb][q0, q1, q1 - q0][k-step] (q slots 0, 1, 3)
+  i32x4 qa[NHB][3][2];
+  const int8_t *qsrc = p.q_pieces + (int64_t)t * NHB * kQBlockBytes + lane * 16;
+#pragma unroll
+  for (int hb = 0; hb < NHB; ++hb)
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        qa[hb][pl][ks] = load_chunk(qsrc + hb * kQBlockBytes + ((pl == 2 ? 3 : pl) * 2 + ks) * kChunk);
+  float wl[NHB][4];
+  const float *wsrc = p.w + (int64_t)t * p.Hi + g * (p.Hi >> 2);
+#pragma unroll
+  for (int hb = 0; hb < NHB; ++hb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wl[hb][i] = wsrc[4 * hb + i];
+
+  // B operands [k0, k1, k0 - k1][k-step] of a block (k slots 0, 1, 2)
+  i32x4 kbuf[3][3][2];
+  auto fetch_k = [&](int b, i32x4 (&k)[3][2]) {
+    b = min(b, bend - 1);
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        k[pl][ks] = __builtin_bit_cast(
+            i32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, lane * 16,
+                                                         b * kBlockBytes + (pl * 2 + ks) * kChunk, 0));
+  };
+  // c_s of the pair starting at block q: lane groups g and g ^ 2 hold block q + (g & 1)
+  auto fetch_cs = [&](int q) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srs, pair4 + q * 64, 0, 0));
+  };
+  struct Acc {
+    i32x4 P00, C3, P11;
+  };
+  Acc acc[3];
+  auto mm = [&](const i32x4 (&k)[3][2], int hb, Acc &a) {
+    const i32x4 z = {0, 0, 0, 0};
+    a.P00 = mfma(qa[hb][0][1], k[0][1], mfma(qa[hb][0][0], k[0][0], z));
+    a.P11 = mfma(qa[hb][1][1], k[1][1], mfma(qa[hb][1][0], k[1][0], z));
+    a.C3 = mfma(qa[hb][2][1], k[2][1], mfma(qa[hb][2][0], k[2][0], a.P00));
+  };
+  // D = ((C3 + 129 P11) << 7) + P00, then the ReLU, the conversion and the
+  // head's fused multiply-add into the group sum
+  auto epi = [&](const Acc &a, int hb, float &G) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t hi = (uint32_t)__mul24(a.P11[i], 129) + (uint32_t)a.C3[i];
+      const int D = (int)((hi << sh7) + (uint32_t)a.P00[i]);
+      G = __builtin_fmaf(wl[hb][i], (float)max(D, 0), G);
+    }
+  };
+  float G[2] = {0.f, 0.f};  // the lane's group sums of the current pair's blocks
+  // the pair starting at block q: (G0 + G1) + (G2 + G3) of both blocks, times
+  // c_s, stored by lane groups 0 and 1; `last` masks the positions past the
+  // causal limit and a second block at or past bend
+  auto store_pair = [&](int q, float cs, bool last) {
+    auto x = __builtin_amdgcn_permlane16_swap(__float_as_uint(G[0]), __float_as_uint(G[1]), false, false);
+    const float a = __uint_as_float(x[0]) + __uint_as_float(x[1]);  // rows: G0+G1 | G2+G3 of q, q+1
+    auto y = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+    const float total = __uint_as_float(y[0]) + __uint_as_float(y[1]);  // block q + (g & 1)
+    float v = total * cs;
+    const int blk = q + (g & 1);
+    uint32_t off = g < 2 ? pair4 + q * 64 : kDropped;
+    if (last) {
+      if (blk * 16 + col > lim) v = -INFINITY;
+      if (blk >= bend) off = kDropped;
+    }
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ors, off, 0, 0);
+  };
+
+  float cs_pair[3];  // scales of the pairs starting at slots 0, 2, 4
+  fetch_k(b0, kbuf[0]);
+  fetch_k(b0 + 1, kbuf[1]);
+  fetch_k(b0 + 2, kbuf[2]);
+  cs_pair[0] = fetch_cs(b0);
+  {  // block b0 (slot 0; the stages fetch two blocks ahead)
+    float Gc = 0.f;
+#pragma unroll
+    for (int hb = 0; hb < NHB; ++hb) {
+      if (hb >= 2) epi(acc[(hb - 2) % 3], hb - 2, Gc);
+      mm(kbuf[0], hb, acc[hb % 3]);
+    }
+    G[0] = Gc;
+  }
+  // block b, SLOT = (b - b0) mod 6: fetch block b + 2, finish block b - 1
+  // (and, for an even SLOT, store the pair b - 2, b - 1), issue block b's MFMAs
+  auto stage = [&](int b, auto slot_c) {
+    constexpr int SLOT = decltype(slot_c)::value;
+    constexpr bool kEven = (SLOT & 1) == 0;
+    fetch_k(b + 2, kbuf[(SLOT + 2) % 3]);
+    if constexpr (kEven) {
+      cs_pair[SLOT / 2] = fetch_cs(b);
+      __builtin_amdgcn_sched_group_barrier(0x020, 7, 0);
+    } else {
+      __builtin_amdgcn_sched_group_barrier(0x020, 6, 0);
+    }
+    float Gc = 0.f;
+#pragma unroll
+    for (int hb = 0; hb < NHB; ++hb) {
+      const int j = SLOT * NHB + hb;
+      if (hb < 2) {
+        epi(acc[(j + 1) % 3], hb + NHB - 2, G[(SLOT + 1) & 1]);
+        if (kEven && hb == 1) store_pair(b - 2, cs_pair[(SLOT / 2 + 2) % 3], false);
+      } else {
+        epi(acc[(j + 1) % 3], hb - 2, Gc);
+      }
+      mm(kbuf[SLOT % 3], hb, acc[j % 3]);
+      if (kEven && hb == 1) {
+        mfma_valu_groups<6, 4>();
+        __builtin_amdgcn_sched_group_barrier(0x040, 1, 0);
+      } else {
+        mfma_valu_groups<6, 3>();
+      }
+      // the pipeline above pairs each head block's MFMAs with finished
+      // accumulators: nothing moves between head blocks (an MFMA moved
+      // earlier would wait for operands loaded in the same iteration)
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    G[SLOT & 1] = Gc;
+  };
+  // after the range's last block (b - b0 = SLOT mod 6): its last two head
+  // blocks, then its pair
+  auto drain = [&](auto slot_c, int last) {
+    constexpr int SLOT = decltype(slot_c)::value;
+    constexpr int j = SLOT * NHB + NHB - 1;
+    epi(acc[(j + 2) % 3], NHB - 2, G[SLOT & 1]);
+    epi(acc[j % 3], NHB - 1, G[SLOT & 1]);
+    store_pair(last - (SLOT & 1), cs_pair[SLOT / 2], true);
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  using S3 = std::integral_constant<int, 3>;
+  using S4 = std::integral_constant<int, 4>;
+  using S5 = std::integral_constant<int, 5>;
+  int b = b0 + 1;  // b - b0 = 1 mod 6
+  for (; b + 5 < bend; b += 6) {
+    stage(b, S1{});
+    stage(b + 1, S2{});
+    stage(b + 2, S3{});
+    stage(b + 3, S4{});
+    stage(b + 4, S5{});
+    stage(b + 5, S0{});
+  }
+  const int rest = bend - b;  // 0 .. 5 blocks, slots 1 .. rest
+  if (rest > 0) stage(b, S1{});
+  if (rest > 1) stage(b + 1, S2{});
+  if (rest > 2) stage(b + 2, S3{});
+  if (rest > 3) stage(b + 3, S4{});
+  if (rest > 4) stage(b + 4, S5{});
+  switch (rest) {
+    case 0: drain(S0{}, bend - 1); break;
+    case 1: drain(S1{}, bend - 1); break;
+    case 2: drain(S2{}, bend - 1); break;
+    case 3: drain(S3{}, bend - 1); break;
+    case 4: drain(S4{}, bend - 1); break;
+    default: drain(S5{}, bend - 1); break;
+  }
+}
+
 template <int NHB>
 __global__ __launch_bounds__(kScoreWaves * 64) void dsa_idx_score_kernel(IndexerParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -394,8 +651,26 @@ __global__ __launch_bounds__(kScoreWaves * 64) void dsa_idx_score_kernel(Indexer
   int qmax = 0;
 #pragma unroll
   for (int j = 0; j < NHB; ++j) qmax = max(qmax, p.q_max[t * NHB + j]);
-  if (qmax >= kTwoPieceLimit) score_range<NHB, 3>(p, t, b0, b1, qmax);
-  else score_range<NHB, 2>(p, t, b0, b1, qmax);
+  if (qmax >= kTwoPieceLimit) {
+    score_range<NHB, 3>(p, t, b0, b1, qmax);
+    return;
+  }
+  // the range's largest block bound decides whether every block takes the
+  // two-piece int32 path
+  if constexpr (NHB >= 2) {
+    const int lane = threadIdx.x & 63;
+    int rmax = 0;
+    for (int b = b0 + lane; b < b1; b += 64) rmax = max(rmax, p.k_max[b]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) rmax = max(rmax, __shfl_xor(rmax, o));
+    rmax = __builtin_amdgcn_readfirstlane(rmax);
+    const bool descriptors_fit = (int64_t)nkb * kBlockBytes < (1LL << 31);
+    if (rmax < kTwoPieceLimit && (int64_t)qmax * rmax * kIdxDim < (1LL << 31) && descriptors_fit) {
+      score_range_fast<NHB>(p, t, b0, b1);
+      return;
+    }
+  }
+  score_range<NHB, 2>(p, t, b0, b1, qmax);
 }
 
 // ---- top-k ---------------------------------------------------------------

@@ -76,21 +76,21 @@ hipError_t launch_attention_merge(const AttnParams &p, hipStream_t stream);
 // Lightning indexer.  Workspace layout (see indexer_workspace_layout):
 //   k_pieces [ceil(S/16)][3 pieces][2 k-steps][1024 B]  MFMA B operands, lane order
 //   k_max    [ceil(S/16)]                               max |value * 2^9| per block
-//   q_pieces [T][Hi/16][3 pieces][2 k-steps][1024 B]    MFMA A operands, lane order
+//   q_pieces [T][Hi/16][4 planes][2 k-steps][1024 B]    MFMA A operands, lane order
 //   q_max    [T][Hi/16]                                 max |value * 2^9| per 16 heads
-//   k_scale  [S] fp32                                   scales gathered from a paged K cache
+//   k_cs     [S] fp32                                   c_s = fl32(k_scale * 2^-18) per position
 //   scores   [T][S] fp32                                (unless the caller's)
 struct IndexerParams {
   const uint8_t *q;       // [T][Hi][128] e4m3 codes
   const uint8_t *k;       // [S][128] e4m3 codes (or null: paged cache below)
-  const float *k_scale;   // [S] (the workspace copy for a paged cache)
+  const float *k_scale;   // [S] (null with a paged cache)
   // paged K cache: position s is token s % k_page_size of page k_pages[s /
   // k_page_size]; codes at page*k_page_size*132 + off*128, the fp32 scale at
   // page*k_page_size*132 + k_page_size*128 + off*4
   const uint8_t *k_cache;
   const int32_t *k_pages;
   int32_t k_page_size;
-  float *k_scale_ws;      // [S] gathered scales (paged cache)
+  float *k_cs;            // [S] workspace: c_s = fl32(k_scale * 2^-18), written by the prep kernel
   const float *w;         // [T][Hi]
   const int32_t *limit;   // [T]
   int32_t T, Hi, S, topk;
@@ -107,7 +107,7 @@ struct IndexerParams {
 };
 
 struct IndexerWorkspace {
-  size_t k_pieces, k_max, q_pieces, q_max, k_scale, scores, total;  // byte offsets; total = size
+  size_t k_pieces, k_max, q_pieces, q_max, k_cs, scores, total;  // byte offsets; total = size
 };
 
 // Offsets of the indexer's workspace regions; scores are left out when the

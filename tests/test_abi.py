@@ -214,11 +214,11 @@ def test_indexer_workspace_and_empty_call():
         return (x + 255) // 256 * 256
 
     kb, qb = 32768 // 16, 64 * 64 // 16
-    want = (up(kb * 6144) + up(kb * 4) + up(qb * 6144) + up(qb * 4) + up(32768 * 4)
+    want = (up(kb * 6144) + up(kb * 4) + up(qb * 8192) + up(qb * 4) + up(32768 * 4)
             + up(64 * 32768 * 4))
     assert lib.dsa_indexer_workspace_bytes(64, 64, 128, 32768) == want
     kb, qb = (1000 + 15) // 16, 3 * 48 // 16
-    want = up(kb * 6144) + up(kb * 4) + up(qb * 6144) + up(qb * 4) + up(1000 * 4) + up(3 * 1000 * 4)
+    want = up(kb * 6144) + up(kb * 4) + up(qb * 8192) + up(qb * 4) + up(1000 * 4) + up(3 * 1000 * 4)
     assert lib.dsa_indexer_workspace_bytes(3, 48, 128, 1000) == want
     assert lib.dsa_indexer_topk(ctypes.byref(_idx_args(num_tokens=0, q_idx=None)), None) == 0
 
