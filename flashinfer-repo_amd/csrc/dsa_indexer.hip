@@ -82,7 +82,7 @@ constexpr int kKTokenBytes = kIdxDim + 4;  // paged K cache: codes + fp32 scale 
 constexpr int kChunk = 1024;              // one MFMA operand: 64 lanes x 16 bytes
 constexpr int kBlockBytes = 3 * 2 * kChunk;  // k block: 3 planes x 2 k-steps
 constexpr int kQBlockBytes = 4 * 2 * kChunk; // q head block: 4 planes x 2 k-steps
-constexpr int kPrepThreads = 256;         // two 16-row blocks x 8 segments of 16 bytes
+constexpr int kPrepThreads = 256;         // four waves, one destination block each
 constexpr int kScoreWaves = 8;            // tokens per score workgroup
 constexpr int kTargetScoreWaves = 2048;   // two waves per SIMD on 256 CUs
 constexpr int kMinBlocksPerWave = 8;
@@ -118,9 +118,11 @@ __device__ __forceinline__ i32x4 mfma(i32x4 a, i32x4 b, i32x4 c) {
 
 // ---- operand preparation -------------------------------------------------
 //
-// Row blocks 0 .. ceil(S/16)-1 are k blocks (16 positions); the following
-// T*Hi/16 blocks are q blocks (token t, heads 16j .. 16j+15).  Thread layout:
-// row r = (tid >> 3) & 15 of block (tid >> 7), 16-byte segment tid & 7.
+// Destination blocks 0 .. ceil(S/16)-1 are k blocks (16 positions); the
+// following T*Hi/16 are q head blocks (token t, head block hb).  One wave
+// prepares one destination block; lane l = 16*g + c loads the 2 x 16 bytes it
+// writes: row c at dims 64*ks + 16*g for k-steps ks = 0, 1, so every plane
+// store of the wave is one contiguous 1 KB operand chunk.
 //
 // An operand chunk holds, for lane l = 16*g + c, the 16 bytes of k-step ks
 // (64 dims) starting at dim 16*g: of position 16*block + c (B operand), or of
@@ -131,93 +133,90 @@ __device__ __forceinline__ i32x4 mfma(i32x4 a, i32x4 b, i32x4 c) {
 __global__ __launch_bounds__(kPrepThreads) void dsa_idx_prep_kernel(IndexerParams p) {
   // code -> signed bytes p0 | p1 << 8 | p2 << 16 | (p0 - p1) << 24
   __shared__ uint32_t lut[256];
-  __shared__ uint32_t s_max[2];  // largest magnitude code (code & 0x7f) of each row block
   {
     const int x = e4m3_x(threadIdx.x);
     const uint32_t b0 = piece_byte(x, 0), b1 = piece_byte(x, 1);
     const uint32_t d = (uint32_t)((int)(int8_t)b0 - (int)(int8_t)b1) & 0xffu;
     lut[threadIdx.x] = b0 | (b1 << 8) | (piece_byte(x, 2) << 16) | (d << 24);
   }
-  if (threadIdx.x < 2) s_max[threadIdx.x] = 0;
+  __syncthreads();
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nkb = (p.S + 15) >> 4, nqb = p.Hi >> 4;
-  const int local = threadIdx.x >> 7;
-  const int rb = blockIdx.x * 2 + local;
-  const int r = (threadIdx.x >> 3) & 15, seg = threadIdx.x & 7;
   const int total = nkb + p.T * nqb;
-  const bool active = rb < total;
-  const bool is_k = rb < nkb;
+  const int blk = blockIdx.x * (kPrepThreads / 64) + wave;
+  if (blk >= total) return;
+  const bool is_k = blk < nkb;
 
-  uint4 raw = make_uint4(0, 0, 0, 0);
-  int t = 0, h = 0;
-  if (active) {
-    if (is_k) {
-      const int s = rb * 16 + r;
-      if (s < p.S) {
-        if (p.k_cache != nullptr) {  // paged: codes, and the scale copied to the workspace
-          const int pg = p.k_pages[s / p.k_page_size], off = s % p.k_page_size;
-          const uint8_t *page = p.k_cache + (int64_t)pg * p.k_page_size * kKTokenBytes;
-          raw = *(const uint4 *)(page + off * kIdxDim + seg * 16);
-          if (seg == 0) p.k_cs[s] = *(const float *)(page + p.k_page_size * kIdxDim + off * 4) * 0x1p-18f;
-        } else {
-          raw = *(const uint4 *)(p.k + (int64_t)s * kIdxDim + seg * 16);
-          if (seg == 0) p.k_cs[s] = p.k_scale[s] * 0x1p-18f;
-        }
+  uint4 raw[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+  int8_t *dst;
+  if (is_k) {
+    const int s = blk * 16 + c;
+    if (s < p.S) {
+      if (p.k_cache != nullptr) {  // paged: codes and scale through the page map
+        const int pg = p.k_pages[s / p.k_page_size], off = s % p.k_page_size;
+        const uint8_t *page = p.k_cache + (int64_t)pg * p.k_page_size * kKTokenBytes;
+        raw[0] = *(const uint4 *)(page + off * kIdxDim + g * 16);
+        raw[1] = *(const uint4 *)(page + off * kIdxDim + 64 + g * 16);
+        if (g == 0) p.k_cs[s] = *(const float *)(page + p.k_page_size * kIdxDim + off * 4) * 0x1p-18f;
+      } else {
+        const uint8_t *row = p.k + (int64_t)s * kIdxDim;
+        raw[0] = *(const uint4 *)(row + g * 16);
+        raw[1] = *(const uint4 *)(row + 64 + g * 16);
+        if (g == 0) p.k_cs[s] = p.k_scale[s] * 0x1p-18f;
       }
-    } else {
-      const int qb = rb - nkb;
-      t = qb / nqb;
-      h = (qb % nqb) * 16 + r;
-      raw = *(const uint4 *)(p.q + ((int64_t)t * p.Hi + h) * kIdxDim + seg * 16);
     }
+    dst = p.k_pieces + (int64_t)blk * kBlockBytes + lane * 16;
+  } else {
+    const int qb = blk - nkb, t = qb / nqb, hb = qb % nqb;
+    const int head = (c >> 2) * (p.Hi >> 2) + 4 * hb + (c & 3);
+    const uint8_t *row = p.q + ((int64_t)t * p.Hi + head) * kIdxDim;
+    raw[0] = *(const uint4 *)(row + g * 16);
+    raw[1] = *(const uint4 *)(row + 64 + g * 16);
+    dst = p.q_pieces + (int64_t)qb * kQBlockBytes + lane * 16;
   }
-  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
   // e4m3 magnitudes order like their codes & 0x7f; the NaN code 0x7f ranks
   // above 448, which only makes the block's bound conservative
+  const uint32_t w[8] = {raw[0].x, raw[0].y, raw[0].z, raw[0].w, raw[1].x, raw[1].y, raw[1].z, raw[1].w};
   uint32_t mc = 0;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) mc = max(mc, (w[i >> 2] >> (8 * (i & 3))) & 0x7fu);
-  __syncthreads();
-  atomicMax(&s_max[local], mc);
-  __syncthreads();
-  if (!active) return;
-  const uint32_t top = s_max[local];
+  for (int i = 0; i < 32; ++i) mc = max(mc, (w[i >> 2] >> (8 * (i & 3))) & 0x7fu);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mc = max(mc, (uint32_t)__shfl_xor((int)mc, o));
+  const uint32_t top = __builtin_amdgcn_readfirstlane(mc);
   const int bmax = top == 0x7f ? (15 << 14) : e4m3_x(top);
-
-  // Planes (slot <- LUT byte).  k block: p0, p1, then p2 if the block holds
-  // a value of magnitude >= 32, else p0 - p1 (slot 2 is read as p2 only for
-  // such blocks).  q head block: p0, p1, p2, and in slot 3 p1 - p0 when every
-  // value of the 16 heads is below 32.
   const bool two = bmax < kTwoPieceLimit;
-  int8_t *dst;
-  const int ks = seg >> 2, g = seg & 3;
-  if (is_k) {
-    dst = p.k_pieces + (int64_t)rb * kBlockBytes + ks * kChunk + (16 * g + r) * 16;
-    if (r == 0 && seg == 0) p.k_max[rb] = bmax;
-  } else {
-    const int quarter = p.Hi >> 2;
-    const int gq = h / quarter, within = h % quarter;
-    const int hb = within >> 2, row = 4 * gq + (within & 3);
-    dst = p.q_pieces + ((int64_t)t * nqb + hb) * kQBlockBytes + ks * kChunk + (16 * g + row) * 16;
-    if (r == 0 && seg == 0) p.q_max[rb - nkb] = bmax;
+  if (lane == 0) {
+    if (is_k) p.k_max[blk] = bmax;
+    else p.q_max[blk - nkb] = bmax;
   }
-  uint32_t v[16];
+
+  uint32_t v[32];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) v[i] = lut[(w[i >> 2] >> (8 * (i & 3))) & 0xffu];
+  for (int i = 0; i < 32; ++i) v[i] = lut[(w[i >> 2] >> (8 * (i & 3))) & 0xffu];
+  // plane `slot` of both k-steps from LUT byte `byte` (negated: q's q1 - q0)
   auto put = [&](int slot, int byte, bool negate) {
-    uint32_t o[4];
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      uint32_t packed = 0;
+    for (int ks = 0; ks < 2; ++ks) {
+      uint32_t o[4];
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        uint32_t x = (v[4 * d + b] >> (8 * byte)) & 0xffu;
-        if (negate) x = (0u - x) & 0xffu;
-        packed |= x << (8 * b);
+      for (int d = 0; d < 4; ++d) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          uint32_t x = (v[16 * ks + 4 * d + b] >> (8 * byte)) & 0xffu;
+          if (negate) x = (0u - x) & 0xffu;
+          packed |= x << (8 * b);
+        }
+        o[d] = packed;
       }
-      o[d] = packed;
+      *(uint4 *)(dst + (slot * 2 + ks) * kChunk) = make_uint4(o[0], o[1], o[2], o[3]);
     }
-    *(uint4 *)(dst + slot * 2 * kChunk) = make_uint4(o[0], o[1], o[2], o[3]);
   };
+  // k block: p0, p1, then p2 if the block holds a value of magnitude >= 32,
+  // else p0 - p1 (slot 2 is read as p2 only for such blocks).  q head block:
+  // p0, p1, p2, and in slot 3 p1 - p0 when every value of its 16 heads is
+  // below 32.
   put(0, 0, false);
   put(1, 1, false);
   if (is_k) {
@@ -1120,7 +1119,7 @@ hipError_t launch_indexer(const IndexerParams &pin, hipStream_t stream) {
   if (pin.T == 0) return hipSuccess;
   IndexerParams p = pin;
   const int nkb = (p.S + 15) / 16, nqb = p.Hi / 16;
-  const int prep_blocks = (nkb + p.T * nqb + 1) / 2;
+  const int prep_blocks = (nkb + p.T * nqb + kPrepThreads / 64 - 1) / (kPrepThreads / 64);
   hipLaunchKernelGGL(dsa_idx_prep_kernel, dim3(prep_blocks), dim3(kPrepThreads), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
