@@ -23,11 +23,14 @@
 //   D = sum_{a,b} 2^(7(a+b)) sum_j pq_a[j] pk_b[j]
 // where each inner 128-term sum (|.| <= 128*127*127) is exact in the int32
 // accumulator of v_mfma_i32_16x16x64_i8.  When every |x| < 2^14 (values below
-// 32) the third piece is zero; four piece products remain, the two cross
-// products accumulate in one MFMA chain, and D = P00 + 2^7 X + 2^14 P11 is
-// combined in int32 when the operand maxima bound |D| below 2^31, else in
-// fp64.  Larger values take nine products and an fp64 combine (exact: every
-// partial sum stays below 2^50).  e4m3fn NaN codes (0x7f, 0xff) count as zero.
+// 32) the third piece is zero and D = P00 + 2^7 X + 2^14 P11 (X the two cross
+// products) is combined in int32 when the operand maxima bound |D| below
+// 2^31, else in fp64.  Where a whole range of positions allows the int32
+// combine, three products suffice: the pieces lie in [0, 127] with the
+// value's sign, so q1 - q0 and k0 - k1 fit int8 and C3 = P00 + (q1 - q0).(k0
+// - k1) = X - P11 gives D = ((C3 + 129 P11) << 7) + P00.  Larger values take
+// nine products and an fp64 combine (exact: every partial sum stays below
+// 2^50).  e4m3fn NaN codes (0x7f, 0xff) count as zero.
 //
 // Kernels:
 //   dsa_idx_prep_kernel    q and k codes -> piece planes laid out as MFMA
