@@ -40,16 +40,17 @@
 //                          in a contiguous workspace array.  With a paged K
 //                          cache it reads each position's codes and scale
 //                          through the page map.
-//   dsa_idx_score_kernel   one wave per query token, up to 8 tokens per
+//   dsa_idx_score_kernel   two waves per query token, up to 4 tokens per
 //                          workgroup sharing a range of positions.  The
 //                          token's q pieces stay in registers (A operands,
 //                          heads as M); each 16-position block's k pieces are
 //                          one coalesced 1 KB load per operand (B, positions
-//                          as N).  No LDS and no barriers.  When every block
-//                          of a wave's range takes the two-piece int32 path
-//                          the loop is software-pipelined: a head block's
-//                          MFMAs are issued beside the previous head block's
-//                          epilogue.
+//                          as N).  When every block of the range takes the
+//                          three-product int32 path, the token's two waves
+//                          claim chunks of six blocks from a counter in LDS
+//                          and the loop is software-pipelined: a head block's
+//                          MFMAs are issued beside the epilogue of the head
+//                          block two before it.
 //   dsa_idx_topk_kernel    one workgroup per row, the row in registers
 //                          (loaded coalesced, 1024-strided, through one
 //                          buffer descriptor): two radix passes (8 bits each,
@@ -86,7 +87,7 @@ constexpr int kChunk = 1024;              // one MFMA operand: 64 lanes x 16 byt
 constexpr int kBlockBytes = 3 * 2 * kChunk;  // k block: 3 planes x 2 k-steps
 constexpr int kQBlockBytes = 4 * 2 * kChunk; // q head block: 4 planes x 2 k-steps
 constexpr int kPrepThreads = 256;         // four waves, one destination block each
-constexpr int kScoreWaves = 8;            // tokens per score workgroup
+constexpr int kScoreWaves = 8;            // waves per score workgroup (two per token)
 constexpr int kTargetScoreWaves = 2048;   // two waves per SIMD on 256 CUs
 constexpr int kMinBlocksPerWave = 8;
 constexpr int kTopkThreads = 1024;
@@ -438,15 +439,22 @@ __device__ __forceinline__ void mfma_valu_groups() {
 // arithmetic is modulo 2^32 and D itself fits int32).  The int8 MFMA path
 // is bound by the chip's power limit, not by issue: fewer MFMAs are faster.
 //
-// Software-pipelined over the range's head blocks j = (b - b0) * NHB + hb:
-// the six MFMAs of head block j are issued between the epilogue
-// instructions of head block j - 2, whose accumulators are complete by then.
-// The loop is unrolled by six blocks, so the three accumulator sets (j mod
-// 3), the three operand buffers (block mod 3, fetched two blocks ahead), the
-// group sums G[block mod 2] and the pair scales all have static indices.  A
-// pair of blocks shares one reduction over the four lane groups (a
-// permlane16 swap of the two blocks' sums, a permlane32 swap, two adds: lane
-// groups 0 and 1 end with blocks q and q + 1), one scale load and one store.
+// Two waves share the token's range (the two waves of one SIMD: one of
+// them is issued first, and with fixed halves it would finish long before
+// the other, which then runs alone): each claims chunks of six blocks from
+// the pair's counter in LDS (`claim`, counting blocks from b0), one chunk
+// ahead, until the range is used up.  Claims only grow, so every wave ends.
+//
+// Software-pipelined over the wave's sequence of head blocks j: the six
+// MFMAs of head block j are issued between the epilogue instructions of head
+// block j - 2, whose accumulators are complete by then; the pipeline runs
+// on across chunk boundaries.  A chunk holds six blocks, so the three
+// accumulator sets (j mod 3), the three operand buffers (fetched two blocks
+// ahead), the group sums G[slot mod 2] and the pair scales, indexed by a
+// block's slot in its chunk, all have static indices.  A pair of blocks
+// shares one reduction over the four lane groups (a permlane16 swap of the
+// two blocks' sums, a permlane32 swap, two adds: lane groups 0 and 1 end
+// with blocks q and q + 1), one scale load and one store.
 //
 // Loads and stores go through buffer descriptors with scalar block offsets;
 // scale loads and score stores carry the position in the per-lane offset,
@@ -455,7 +463,8 @@ __device__ __forceinline__ void mfma_valu_groups() {
 // loaded: a wave-uniform loaded value is moved to a scalar register right
 // after its load, a wait that would tie each prefetch to its own step.
 template <int NHB>
-__device__ __forceinline__ void score_range_fast(const IndexerParams &p, int t, int b0, int b1) {
+__device__ __forceinline__ void score_range_fast(const IndexerParams &p, int t, int b0, int b1,
+                                                 int *claim, bool lead) {
 #pragma clang fp contract(off)
   static_assert(NHB >= 2, "the epilogue runs two head blocks behind");
   const int lane = threadIdx.x & 63;
@@ -475,10 +484,19 @@ __device__ __forceinline__ void score_range_fast(const IndexerParams &p, int t, 
   // blocks [b0, bend) hold a position at or below the causal limit; every
   // position of the blocks before bend - 1 is below it
   const int bend = min(b1, max(b0, (lim >> 4) + 1));
-  for (int b = bend; b < b1; ++b)
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(-INFINITY), ors,
-                                          g == 0 ? col * 4 + b * 64 : kDropped, 0, 0);
-  if (bend == b0) return;
+  if (lead)
+    for (int b = bend; b < b1; ++b)
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(-INFINITY), ors,
+                                            g == 0 ? col * 4 + b * 64 : kDropped, 0, 0);
+  // first block of the next chunk of six the pair has not claimed yet
+  auto claim_chunk = [&]() {
+    int c = 0;
+    if (lane == 0) c = atomicAdd(claim, 6);
+    return b0 + __builtin_amdgcn_readfirstlane(c);
+  };
+  int B = claim_chunk();  // the current chunk
+  if (B >= bend) return;
+  int N = claim_chunk();  // the next one
 
   // A operands [hb][q0, q1, q1 - q0][k-step] (q slots 0, 1, 3)
   i32x4 qa[NHB][3][2];
@@ -553,11 +571,11 @@ __device__ __forceinline__ void score_range_fast(const IndexerParams &p, int t, 
   };
 
   float cs_pair[3];  // scales of the pairs starting at slots 0, 2, 4
-  fetch_k(b0, kbuf[0]);
-  fetch_k(b0 + 1, kbuf[1]);
-  fetch_k(b0 + 2, kbuf[2]);
-  cs_pair[0] = fetch_cs(b0);
-  {  // block b0 (slot 0; the stages fetch two blocks ahead)
+  fetch_k(B, kbuf[0]);
+  fetch_k(B + 1, kbuf[1]);
+  fetch_k(B + 2, kbuf[2]);
+  cs_pair[0] = fetch_cs(B);
+  {  // block B (slot 0; the stages fetch two blocks ahead)
     float Gc = 0.f;
 #pragma unroll
     for (int hb = 0; hb < NHB; ++hb) {
@@ -566,12 +584,14 @@ __device__ __forceinline__ void score_range_fast(const IndexerParams &p, int t, 
     }
     G[0] = Gc;
   }
-  // block b, SLOT = (b - b0) mod 6: fetch block b + 2, finish block b - 1
-  // (and, for an even SLOT, store the pair b - 2, b - 1), issue block b's MFMAs
-  auto stage = [&](int b, auto slot_c) {
+  // block b in slot SLOT of its chunk: fetch the block two ahead (`ahead`:
+  // past the chunk, in the next one), finish the previous block (and, for an
+  // even SLOT, store the pair before it, which starts at `pair`), issue block
+  // b's MFMAs
+  auto stage = [&](int b, auto slot_c, int ahead, int pair) {
     constexpr int SLOT = decltype(slot_c)::value;
     constexpr bool kEven = (SLOT & 1) == 0;
-    fetch_k(b + 2, kbuf[(SLOT + 2) % 3]);
+    fetch_k(ahead, kbuf[(SLOT + 2) % 3]);
     if constexpr (kEven) {
       cs_pair[SLOT / 2] = fetch_cs(b);
       __builtin_amdgcn_sched_group_barrier(0x020, 7, 0);
@@ -584,7 +604,7 @@ __device__ __forceinline__ void score_range_fast(const IndexerParams &p, int t, 
       const int j = SLOT * NHB + hb;
       if (hb < 2) {
         epi(acc[(j + 1) % 3], hb + NHB - 2, G[(SLOT + 1) & 1]);
-        if (kEven && hb == 1) store_pair(b - 2, cs_pair[(SLOT / 2 + 2) % 3], false);
+        if (kEven && hb == 1) store_pair(pair, cs_pair[(SLOT / 2 + 2) % 3], false);
       } else {
         epi(acc[(j + 1) % 3], hb - 2, Gc);
       }
@@ -602,7 +622,7 @@ __device__ __forceinline__ void score_range_fast(const IndexerParams &p, int t, 
     }
     G[SLOT & 1] = Gc;
   };
-  // after the range's last block (b - b0 = SLOT mod 6): its last two head
+  // after the wave's last block (slot SLOT of its chunk): its last two head
   // blocks, then its pair
   auto drain = [&](auto slot_c, int last) {
     constexpr int SLOT = decltype(slot_c)::value;
@@ -617,48 +637,63 @@ __device__ __forceinline__ void score_range_fast(const IndexerParams &p, int t, 
   using S3 = std::integral_constant<int, 3>;
   using S4 = std::integral_constant<int, 4>;
   using S5 = std::integral_constant<int, 5>;
-  int b = b0 + 1;  // b - b0 = 1 mod 6
-  for (; b + 5 < bend; b += 6) {
-    stage(b, S1{});
-    stage(b + 1, S2{});
-    stage(b + 2, S3{});
-    stage(b + 3, S4{});
-    stage(b + 4, S5{});
-    stage(b + 5, S0{});
+  // blocks 1 .. 5 of a full chunk B, then block 0 of the next chunk N
+  while (B + 6 <= bend && N < bend) {
+    const int N2 = claim_chunk();
+    stage(B + 1, S1{}, B + 3, 0);
+    stage(B + 2, S2{}, B + 4, B);
+    stage(B + 3, S3{}, B + 5, 0);
+    stage(B + 4, S4{}, N, B + 2);
+    stage(B + 5, S5{}, N + 1, 0);
+    stage(N, S0{}, N + 2, B + 4);
+    B = N;
+    N = N2;
   }
-  const int rest = bend - b;  // 0 .. 5 blocks, slots 1 .. rest
-  if (rest > 0) stage(b, S1{});
-  if (rest > 1) stage(b + 1, S2{});
-  if (rest > 2) stage(b + 2, S3{});
-  if (rest > 3) stage(b + 3, S4{});
-  if (rest > 4) stage(b + 4, S5{});
+  // the wave's last chunk: blocks 1 .. rest (the operand fetches past it are
+  // clamped to bend - 1 and unused)
+  const int rest = min(bend, B + 6) - 1 - B;
+  if (rest > 0) stage(B + 1, S1{}, B + 3, 0);
+  if (rest > 1) stage(B + 2, S2{}, B + 4, B);
+  if (rest > 2) stage(B + 3, S3{}, B + 5, 0);
+  if (rest > 3) stage(B + 4, S4{}, B + 6, B + 2);
+  if (rest > 4) stage(B + 5, S5{}, B + 7, 0);
   switch (rest) {
-    case 0: drain(S0{}, bend - 1); break;
-    case 1: drain(S1{}, bend - 1); break;
-    case 2: drain(S2{}, bend - 1); break;
-    case 3: drain(S3{}, bend - 1); break;
-    case 4: drain(S4{}, bend - 1); break;
-    default: drain(S5{}, bend - 1); break;
+    case 0: drain(S0{}, B); break;
+    case 1: drain(S1{}, B + 1); break;
+    case 2: drain(S2{}, B + 2); break;
+    case 3: drain(S3{}, B + 3); break;
+    case 4: drain(S4{}, B + 4); break;
+    default: drain(S5{}, B + 5); break;
   }
 }
 
 template <int NHB>
 __global__ __launch_bounds__(kScoreWaves * 64) void dsa_idx_score_kernel(IndexerParams p) {
+  // two waves per token: slot = the token's place in the workgroup, member
+  // 0 or 1 (waves w and w + tpw, which the hardware places on one SIMD)
+  __shared__ int claim[kScoreWaves / 2];
+  const int tpw = blockDim.x >> 7;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int t = blockIdx.y * (blockDim.x >> 6) + wave;
+  const int slot = wave % tpw, member = wave / tpw;
+  if (threadIdx.x < kScoreWaves / 2) claim[threadIdx.x] = 0;
+  __syncthreads();
+  const int t = blockIdx.y * tpw + slot;
   const int nkb = (p.S + 15) >> 4;
   const int b0 = blockIdx.x * p.blocks_per_wg;
   const int b1 = min(nkb, b0 + p.blocks_per_wg);
   if (t >= p.T || b0 >= b1) return;
+  // the general paths split the range in halves
+  const int mid = b0 + (b1 - b0 + 1) / 2;
+  const int h0 = member == 0 ? b0 : mid, h1 = member == 0 ? mid : b1;
   int qmax = 0;
 #pragma unroll
   for (int j = 0; j < NHB; ++j) qmax = max(qmax, p.q_max[t * NHB + j]);
   if (qmax >= kTwoPieceLimit) {
-    score_range<NHB, 3>(p, t, b0, b1, qmax);
+    if (h0 < h1) score_range<NHB, 3>(p, t, h0, h1, qmax);
     return;
   }
   // the range's largest block bound decides whether every block takes the
-  // two-piece int32 path
+  // three-product path
   if constexpr (NHB >= 2) {
     const int lane = threadIdx.x & 63;
     int rmax = 0;
@@ -668,11 +703,11 @@ __global__ __launch_bounds__(kScoreWaves * 64) void dsa_idx_score_kernel(Indexer
     rmax = __builtin_amdgcn_readfirstlane(rmax);
     const bool descriptors_fit = (int64_t)nkb * kBlockBytes < (1LL << 31);
     if (rmax < kTwoPieceLimit && (int64_t)qmax * rmax * kIdxDim < (1LL << 31) && descriptors_fit) {
-      score_range_fast<NHB>(p, t, b0, b1);
+      score_range_fast<NHB>(p, t, b0, b1, &claim[slot], member == 0);
       return;
     }
   }
-  score_range<NHB, 2>(p, t, b0, b1, qmax);
+  if (h0 < h1) score_range<NHB, 2>(p, t, h0, h1, qmax);
 }
 
 // ---- top-k ---------------------------------------------------------------
@@ -1127,16 +1162,17 @@ hipError_t launch_indexer(const IndexerParams &pin, hipStream_t stream) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (p.S > 0) {
-    // tokens per workgroup (one wave each) and 16-position blocks per wave,
-    // aiming at two waves per SIMD with at least 8 blocks per wave
-    const int waves = std::min(p.T, kScoreWaves);
-    const int tgroups = (p.T + waves - 1) / waves;
-    int bx = (kTargetScoreWaves + waves * tgroups - 1) / (waves * tgroups);
-    bx = std::min(bx, (nkb + kMinBlocksPerWave - 1) / kMinBlocksPerWave);
+    // tokens per workgroup (two waves each) and 16-position blocks per
+    // workgroup range, aiming at two waves per SIMD with at least 8 blocks
+    // per wave
+    const int tpw = std::min(p.T, kScoreWaves / 2);
+    const int tgroups = (p.T + tpw - 1) / tpw;
+    int bx = (kTargetScoreWaves + 2 * tpw * tgroups - 1) / (2 * tpw * tgroups);
+    bx = std::min(bx, (nkb + 2 * kMinBlocksPerWave - 1) / (2 * kMinBlocksPerWave));
     bx = std::max(bx, 1);
     p.blocks_per_wg = (nkb + bx - 1) / bx;
     bx = (nkb + p.blocks_per_wg - 1) / p.blocks_per_wg;
-    const dim3 grid(bx, tgroups), block(64 * waves);
+    const dim3 grid(bx, tgroups), block(128 * tpw);
     switch (nqb) {
       case 1: e = launch_score<1>(p, grid, block, stream); break;
       case 2: e = launch_score<2>(p, grid, block, stream); break;
