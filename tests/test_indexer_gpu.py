@@ -73,6 +73,38 @@ def test_ragged_shapes(T, Hi, S, topk):
     _assert_same(got_idx, got_sc, ref_idx, ref_sc, f"T={T} Hi={Hi} S={S} k={topk}")
 
 
+@pytest.mark.parametrize("T,Hi,S", [(22, 32, 3000), (5, 48, 2203), (9, 64, 4099), (1, 64, 900)])
+def test_chunked_ranges_random_causal_limits(T, Hi, S):
+    """Causal limits anywhere in a token's row.  The three-product path deals
+    a range out in chunks of six blocks to the token's two waves; a limit
+    cuts the last chunk after 1..6 blocks (with these shapes every remainder
+    occurs), masks part of its last block and leaves later blocks at -inf.
+    T not a multiple of 4 leaves workgroups with fewer tokens."""
+    d = workloads.indexer_inputs(T=T, Hi=Hi, S=S, seed=T * 7919 + S)
+    lim = np.random.default_rng(S).integers(-3, S, T)
+    d["causal_limit"] = torch.from_numpy(lim.astype(np.int32))
+    topk = min(256, S // 2)
+    got_idx, got_sc = _gpu_indexer(d, topk)
+    ref_idx, ref_sc = _oracle(d, topk)
+    _assert_same(got_idx, got_sc, ref_idx, ref_sc, f"T={T} Hi={Hi} S={S}")
+
+
+@pytest.mark.parametrize("scale,label", [(60.0, "third piece"), (28.0, "beyond the int32 combine")])
+def test_one_wide_block_sends_its_range_to_the_general_paths(scale, label):
+    """One block of 16 positions with large values: the position range that
+    holds it takes the general paths (split between the token's two waves),
+    every other range the three-product path."""
+    T, Hi, S = 6, 64, 5000
+    d = workloads.indexer_inputs(T=T, Hi=Hi, S=S, seed=99)
+    g = torch.Generator().manual_seed(99)
+    k = d["k_idx"].view(torch.float8_e4m3fn).float()
+    k[592:608] = (torch.randn(16, 128, generator=g) * scale).clamp(-scale, scale)
+    d["k_idx"] = workloads.e4m3(k)
+    got_idx, got_sc = _gpu_indexer(d, 300)
+    ref_idx, ref_sc = _oracle(d, 300)
+    _assert_same(got_idx, got_sc, ref_idx, ref_sc, label)
+
+
 def test_ties_go_to_lower_positions():
     d = workloads.indexer_inputs(T=4, Hi=16, S=600, seed=7)
     k = d["k_idx"].clone()
