@@ -222,6 +222,22 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
   const int n_keys = max(0, min(p.K, k_begin + p.chunk) - k_begin);
   const int n_tiles = (n_keys + kKeysPerTile - 1) / kKeysPerTile;
 
+  // Q^T as the B operand of S^T = K Q^T: k-step s covers features 32s..32s+31
+  // (s < 16: q_nope; s = 16, 17: q_pe); this lane holds 8g..8g+7 of them.
+  // Issued before the slot-id staging, whose LDS stores wait for the index
+  // loads: both loads are then in flight together (one memory latency).
+  bf16x8 qreg[R::kQRegs];
+  {
+    const int s0 = Parts<R::kParts>::first(part);
+    const int ns = Parts<R::kParts>::first(part + 1) - s0;
+    const char *qn = p.q_nope + t * p.qn_st + head * p.qn_sh + g * 16;
+    const char *qp = p.q_pe + t * p.qp_st + head * p.qp_sh + g * 16;
+#pragma unroll
+    for (int k = 0; k < R::kQRegs; ++k) {
+      const int s = s0 + k;
+      if (k < ns) qreg[k] = *(const bf16x8 *)(s < 16 ? qn + s * 64 : qp + (s - 16) * 64);
+    }
+  }
   // ---- stage the chunk's slot ids (padding and out-of-range ids -> -1);
   // all index loads are issued before the first store so they overlap
   {
@@ -242,20 +258,6 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
     }
   }
 
-  // Q^T as the B operand of S^T = K Q^T: k-step s covers features 32s..32s+31
-  // (s < 16: q_nope; s = 16, 17: q_pe); this lane holds 8g..8g+7 of them.
-  bf16x8 qreg[R::kQRegs];
-  {
-    const int s0 = Parts<R::kParts>::first(part);
-    const int ns = Parts<R::kParts>::first(part + 1) - s0;
-    const char *qn = p.q_nope + t * p.qn_st + head * p.qn_sh + g * 16;
-    const char *qp = p.q_pe + t * p.qp_st + head * p.qp_sh + g * 16;
-#pragma unroll
-    for (int k = 0; k < R::kQRegs; ++k) {
-      const int s = s0 + k;
-      if (k < ns) qreg[k] = *(const bf16x8 *)(s < 16 ? qn + s * 64 : qp + (s - 16) * 64);
-    }
-  }
   // Retire the Q loads with a wait the compiler sees (s_waitcnt vmcnt(0)), so
   // its own bookkeeping has nothing outstanding when the gather ring starts
   // and it adds no drain at the loop header.
