@@ -80,6 +80,7 @@ namespace dsa {
 namespace {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kIdxDim = 128;
 constexpr int kKTokenBytes = kIdxDim + 4;  // paged K cache: codes + fp32 scale per token
@@ -198,7 +199,9 @@ __global__ __launch_bounds__(kPrepThreads) void dsa_idx_prep_kernel(IndexerParam
   uint32_t v[32];
 #pragma unroll
   for (int i = 0; i < 32; ++i) v[i] = lut[(w[i >> 2] >> (8 * (i & 3))) & 0xffu];
-  // plane `slot` of both k-steps from LUT byte `byte` (negated: q's q1 - q0)
+  // plane `slot` of both k-steps from LUT byte `byte` (negated: q's q1 - q0);
+  // non-temporal stores: the planes are read by the next kernel, and stores
+  // kept in L2 cost a write-back at the kernel's end (measured: 1.6 us of 10.8)
   auto put = [&](int slot, int byte, bool negate) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -214,7 +217,7 @@ __global__ __launch_bounds__(kPrepThreads) void dsa_idx_prep_kernel(IndexerParam
         }
         o[d] = packed;
       }
-      *(uint4 *)(dst + (slot * 2 + ks) * kChunk) = make_uint4(o[0], o[1], o[2], o[3]);
+      __builtin_nontemporal_store(u32x4{o[0], o[1], o[2], o[3]}, (u32x4 *)(dst + (slot * 2 + ks) * kChunk));
     }
   };
   // k block: p0, p1, then p2 if the block holds a value of magnitude >= 32,
