@@ -264,14 +264,6 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
   __builtin_amdgcn_s_waitcnt(0x0F70);
   __syncthreads();  // slot ids visible; nothing gathered yet
 
-  // valid-key mask of tile i in lane i (wave-uniform reads with readlane)
-  uint32_t tile_masks = 0;
-  for (int k = 0; 2 * k < n_tiles; ++k) {
-    const int i = k * 64 + lane;
-    const uint64_t bits = __ballot(i < n_tiles * kKeysPerTile && slots[i] >= 0);
-    tile_masks = lane == 2 * k ? (uint32_t)bits : tile_masks;
-    tile_masks = lane == 2 * k + 1 ? (uint32_t)(bits >> 32) : tile_masks;
-  }
 
   // ---- gather issue: this wave's share of tile j into stage j % kStages.
   // Lane l owns key 8*grp + (l & 7) of the tile, grp being the kpe group
@@ -508,6 +500,16 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
 
   const int pre = min(n_tiles, kStages - 1);
   for (int j = 0; j < pre; ++j) issue_tile(j);
+
+  // valid-key mask of tile i in lane i (wave-uniform reads with readlane),
+  // built while the first tiles are in flight
+  uint32_t tile_masks = 0;
+  for (int k = 0; 2 * k < n_tiles; ++k) {
+    const int i = k * 64 + lane;
+    const uint64_t bits = __ballot(i < n_tiles * kKeysPerTile && slots[i] >= 0);
+    tile_masks = lane == 2 * k ? (uint32_t)bits : tile_masks;
+    tile_masks = lane == 2 * k + 1 ? (uint32_t)(bits >> 32) : tile_masks;
+  }
 
   // Waits until tile i has landed for this wave; the tiles issued after it
   // (up to kStages - 2 of them) may stay in flight.
