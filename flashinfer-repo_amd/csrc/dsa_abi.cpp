@@ -50,7 +50,7 @@ void choose_splits(int64_t T, int64_t H, int64_t K, int32_t requested, int32_t *
   }
   int64_t S;
   int64_t c;
-  const int64_t min_s = ceil_div(K, dsa::kMaxChunk);
+  const int64_t min_s = ceil_div(K, dsa::attn_max_chunk((int)H));
   if (requested > 0) {
     S = requested < K ? requested : K;
     if (S < min_s) S = min_s;

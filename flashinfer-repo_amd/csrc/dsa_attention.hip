@@ -93,11 +93,18 @@ constexpr int kKpeGroupPitch = 1024 + 128;
 constexpr int kCkvStageBytes = kKeysPerTile * kCkvPitch;
 constexpr int kStageBytes = kCkvStageBytes + (kKeysPerTile / 8) * kKpeGroupPitch;
 constexpr int kStages = 4;
-constexpr int kSlotBytes = kMaxChunk * 4;                   // one slot id per key
-constexpr int kXchgBytes = 8 * 64 * 16;                     // one f32x4 per lane per wave
-constexpr int kLdsBytes = kStages * kStageBytes + kSlotBytes + kXchgBytes;
-static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one gfx950 CU");
-static_assert(kMaxChunk / kKeysPerTile <= 64, "one mask lane per tile");
+// After the ring: the chunk's slot ids (4 bytes per key) and, for layouts
+// whose waves share a head group, the partial-score exchange (one f32x4 per
+// lane per wave); one-slice layouts exchange nothing and stage twice the ids.
+template <int FS>
+struct Lds {
+  static constexpr int kMaxChunkKeys = FS == 1 ? kMaxChunkWide : kMaxChunk;
+  static constexpr int kSlotBytes = kMaxChunkKeys * 4;
+  static constexpr int kXchgBytes = FS == 1 ? 0 : 8 * 64 * 16;
+  static constexpr int kBytes = kStages * kStageBytes + kSlotBytes + kXchgBytes;
+  static_assert(kBytes <= 160 * 1024, "LDS budget of one gfx950 CU");
+  static_assert(kMaxChunkKeys / kKeysPerTile <= 64, "one mask lane per tile");
+};
 
 // The running max is only moved (and the accumulator rescaled) when a head's
 // scores exceed it by more than this many log2 units, so probabilities stay
@@ -198,9 +205,10 @@ struct Ring {
 template <int W, int FS>
 __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) {
   using R = Ring<W, FS>;
-  __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
+  using L = Lds<FS>;
+  __shared__ __attribute__((aligned(16))) char lds[L::kBytes];
   int32_t *slots = (int32_t *)(lds + kStages * kStageBytes);  // -1: padding / invalid
-  f32x4 *xbuf = (f32x4 *)(lds + kStages * kStageBytes + kSlotBytes);
+  f32x4 *xbuf = (f32x4 *)(lds + kStages * kStageBytes + L::kSlotBytes);  // FS > 1 only
 
   const int t = blockIdx.x / p.num_splits;
   const int split = blockIdx.x - t * p.num_splits;
@@ -241,7 +249,7 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
   // ---- stage the chunk's slot ids (padding and out-of-range ids -> -1);
   // all index loads are issued before the first store so they overlap
   {
-    constexpr int kPer = kMaxChunk / (W * 64);
+    constexpr int kPer = L::kMaxChunkKeys / (W * 64);
     const int32_t *src = p.idx + (int64_t)t * p.idx_st + k_begin;
     int sv[kPer];
 #pragma unroll
@@ -783,6 +791,11 @@ hipError_t launch_ring(const AttnParams &p, int head_blocks, hipStream_t stream)
 }  // namespace
 
 bool attn_merges_in_kernel(int H) { return (H / kHeadsPerGroup) % 2 != 0; }  // the <8, 8> layout
+
+int attn_max_chunk(int H) {
+  const int groups = H / kHeadsPerGroup;
+  return groups % 4 == 0 ? Lds<1>::kMaxChunkKeys : Lds<2>::kMaxChunkKeys;  // the layouts below
+}
 
 int attn_head_blocks(int H) {
   const int groups = H / kHeadsPerGroup;

@@ -18,6 +18,7 @@ constexpr int kHeadsPerGroup = 16;  // MFMA N dimension: one 16-head group
 constexpr int kKeysPerTile = 32;       // keys gathered into one LDS ring stage
 constexpr int kMinTilesPerSplit = 4;   // automatic splits keep >= 4 tiles of work each
 constexpr int kMaxChunk = 1024;        // top-k entries one workgroup handles (LDS-staged ids)
+constexpr int kMaxChunkWide = 2048;    // the same for one-slice layouts (no score exchange)
 
 struct AttnParams {
   const char *q_nope;  // byte strides below
@@ -61,6 +62,8 @@ inline int64_t attn_counter_words(int64_t T, int head_blocks) { return T * head_
 
 // Workgroups per token along the head axis (each covers up to 8 groups of 16).
 int attn_head_blocks(int H);
+// Longest top-k chunk one workgroup of the layout for H heads handles.
+int attn_max_chunk(int H);
 // Whether split calls with counters merge inside the attention kernel for H
 // heads (the layout with 8 feature slices per head group); otherwise the
 // merge kernel runs and the counters are not touched.
