@@ -93,17 +93,22 @@ constexpr int kKpeGroupPitch = 1024 + 128;
 constexpr int kCkvStageBytes = kKeysPerTile * kCkvPitch;
 constexpr int kStageBytes = kCkvStageBytes + (kKeysPerTile / 8) * kKpeGroupPitch;
 constexpr int kStages = 4;
-// After the ring: the chunk's slot ids (4 bytes per key) and, for layouts
-// whose waves share a head group, the partial-score exchange (one f32x4 per
-// lane per wave); one-slice layouts exchange nothing and stage twice the ids.
+// After the ring: slot ids (4 bytes per key) and, for layouts whose waves
+// share a head group, the partial-score exchange (one f32x4 per lane per
+// wave).  One-slice layouts exchange nothing and stage the ids of a whole
+// 2048-key chunk; the others keep a ring of 32 tiles' ids, refilled half by
+// half while the chunk runs (refill_ids in the kernel).
 template <int FS>
 struct Lds {
-  static constexpr int kMaxChunkKeys = FS == 1 ? kMaxChunkWide : kMaxChunk;
-  static constexpr int kSlotBytes = kMaxChunkKeys * 4;
+  static constexpr int kMaxChunkKeys = kMaxChunkWide;
+  static constexpr int kSlotIds = FS == 1 ? kMaxChunkWide : kMaxChunk;
+  static constexpr int kRingTiles = kSlotIds / kKeysPerTile;
+  static constexpr int kSlotBytes = kSlotIds * 4;
   static constexpr int kXchgBytes = FS == 1 ? 0 : 8 * 64 * 16;
   static constexpr int kBytes = kStages * kStageBytes + kSlotBytes + kXchgBytes;
   static_assert(kBytes <= 160 * 1024, "LDS budget of one gfx950 CU");
   static_assert(kMaxChunkKeys / kKeysPerTile <= 64, "one mask lane per tile");
+  static_assert(kRingTiles % 32 == 0, "refills are halves of 16 tiles");
 };
 
 // The running max is only moved (and the accumulator rescaled) when a head's
@@ -113,10 +118,21 @@ constexpr float kRescaleSlack = 8.0f;
 
 // Padding keys gather from here (global memory, never written).
 __device__ __attribute__((aligned(64))) const uint4 g_zero_row[64] = {};
+// Slot-id refills read keys past the chunk from here: -1, padding.
+__device__ __attribute__((aligned(64))) const int32_t g_minus_one[64] = {
+    -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1,
+    -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1,
+    -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1, -1};
 
 __device__ __forceinline__ void lds_dma16(const void *gsrc, void *ldst) {
   __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)gsrc,
                                    (__attribute__((address_space(3))) void *)ldst, 16, 0, 0);
+}
+
+// 4 bytes per lane: lane i lands at ldst + 4 i.
+__device__ __forceinline__ void lds_dma4(const void *gsrc, void *ldst) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)gsrc,
+                                   (__attribute__((address_space(3))) void *)ldst, 4, 0, 0);
 }
 
 __device__ __forceinline__ bf16x4 lds_read_tr16(const char *p) {
@@ -246,10 +262,11 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
       if (k < ns) qreg[k] = *(const bf16x8 *)(s < 16 ? qn + s * 64 : qp + (s - 16) * 64);
     }
   }
-  // ---- stage the chunk's slot ids (padding and out-of-range ids -> -1);
-  // all index loads are issued before the first store so they overlap
+  // ---- stage the slot ids of the chunk's first kRingTiles tiles (padding and
+  // out-of-range ids -> -1); all index loads are issued before the first
+  // store so they overlap
   {
-    constexpr int kPer = L::kMaxChunkKeys / (W * 64);
+    constexpr int kPer = L::kSlotIds / (W * 64);
     const int32_t *src = p.idx + (int64_t)t * p.idx_st + k_begin;
     int sv[kPer];
 #pragma unroll
@@ -279,11 +296,21 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
   const int grp = (W == 4) ? wave : (wave >> 1);
   const int row0 = (W == 4) ? 0 : 4 * (wave & 1);  // first ckv row within the group
   const uint64_t zero_row = (uint64_t)(const char *)g_zero_row;
+  // valid-key mask of tile i in lane i (wave-uniform reads with readlane):
+  // tiles of the first ring pass are masked after the first gathers are
+  // issued, tiles of refilled ids when they are issued
+  uint32_t tile_masks = 0;
   auto issue_tile = [&](int j) {
     char *st = lds + (j % kStages) * kStageBytes;
-    const int sl = slots[j * kKeysPerTile + grp * 8 + (lane & 7)];
+    const int32_t *ids = slots + (j % L::kRingTiles) * kKeysPerTile;  // refilled ids are raw
+    const int sl = ids[grp * 8 + (lane & 7)];
+    if (FS >= 2 && j >= L::kRingTiles) {
+      const int id = ids[lane & 31];
+      const uint32_t bits = (uint32_t)__ballot(id >= 0 && (int64_t)id < p.num_slots);
+      tile_masks = lane == j ? bits : tile_masks;
+    }
     uint64_t ckv_addr = zero_row, kpe_addr = zero_row;
-    if (sl >= 0) {
+    if (sl >= 0 && (int64_t)sl < p.num_slots) {
       const uint32_t pg = (uint32_t)(((uint64_t)(uint32_t)sl * p.ps_magic) >> (31 + p.ps_shift));
       const uint32_t of = (uint32_t)sl - pg * (uint32_t)p.page_size;
       ckv_addr = (uint64_t)(p.ckv + (int64_t)pg * p.ckv_sp + (int64_t)of * p.ckv_so);
@@ -509,10 +536,8 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
   const int pre = min(n_tiles, kStages - 1);
   for (int j = 0; j < pre; ++j) issue_tile(j);
 
-  // valid-key mask of tile i in lane i (wave-uniform reads with readlane),
-  // built while the first tiles are in flight
-  uint32_t tile_masks = 0;
-  for (int k = 0; 2 * k < n_tiles; ++k) {
+  // the first ring pass's tile masks, built while the first tiles are in flight
+  for (int k = 0; 2 * k < min(n_tiles, L::kRingTiles); ++k) {
     const int i = k * 64 + lane;
     const uint64_t bits = __ballot(i < n_tiles * kKeysPerTile && slots[i] >= 0);
     tile_masks = lane == 2 * k ? (uint32_t)bits : tile_masks;
@@ -550,6 +575,24 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): partial written, tile i-1 read
     __builtin_amdgcn_s_barrier();
     if (i + kStages - 1 < n_tiles) issue_tile(i + kStages - 1);
+    // Ring refill (layouts whose ring holds 32 tiles' ids): once tile J = 16 m
+    // (m >= 1) is issued, every wave has passed a barrier since it read the
+    // ids of tiles J - 16 .. J - 1, so their half of the ring takes the ids of
+    // tiles J + 16 .. J + 31 (one 4-byte DMA per lane; raw ids, checked when
+    // issued).  The DMA completes before the loads of tile J + 1 (in-order
+    // vmcnt) and is visible after that tile's barrier, 14 iterations before
+    // tile J + 16 is issued.  The stage waits meanwhile count one extra load,
+    // which only makes them wait longer.
+    if constexpr (FS >= 2) {
+      static_assert(W == 8, "a half refill is 512 ids, one per lane of 8 waves");
+      const int J = i + kStages - 1;
+      if (J >= 16 && J % 16 == 0 && J + 16 < n_tiles) {
+        const int key = (J + 16) * kKeysPerTile + wave * 64 + lane;  // W == 8: 512 keys
+        const int32_t *src = key < n_keys ? p.idx + (int64_t)t * p.idx_st + k_begin + key
+                                          : g_minus_one + lane;
+        lds_dma4(src, slots + ((J + 16) % L::kRingTiles) * kKeysPerTile + wave * 64);
+      }
+    }
     if constexpr (kShared) {
       softmax_shared(__builtin_amdgcn_readlane(tile_masks, i), p_hi, p_lo);
     } else {
@@ -792,9 +835,9 @@ hipError_t launch_ring(const AttnParams &p, int head_blocks, hipStream_t stream)
 
 bool attn_merges_in_kernel(int H) { return (H / kHeadsPerGroup) % 2 != 0; }  // the <8, 8> layout
 
-int attn_max_chunk(int H) {
-  const int groups = H / kHeadsPerGroup;
-  return groups % 4 == 0 ? Lds<1>::kMaxChunkKeys : Lds<2>::kMaxChunkKeys;  // the layouts below
+int attn_max_chunk(int) {
+  static_assert(Lds<1>::kMaxChunkKeys == Lds<8>::kMaxChunkKeys, "one chunk bound for every layout");
+  return Lds<1>::kMaxChunkKeys;
 }
 
 int attn_head_blocks(int H) {

@@ -17,8 +17,8 @@ constexpr int kHeadDimKpe = 64;
 constexpr int kHeadsPerGroup = 16;  // MFMA N dimension: one 16-head group
 constexpr int kKeysPerTile = 32;       // keys gathered into one LDS ring stage
 constexpr int kMinTilesPerSplit = 4;   // automatic splits keep >= 4 tiles of work each
-constexpr int kMaxChunk = 1024;        // top-k entries one workgroup handles (LDS-staged ids)
-constexpr int kMaxChunkWide = 2048;    // the same for one-slice layouts (no score exchange)
+constexpr int kMaxChunk = 1024;        // slot ids the multi-slice layouts keep in LDS (a ring)
+constexpr int kMaxChunkWide = 2048;    // top-k entries one workgroup handles
 
 struct AttnParams {
   const char *q_nope;  // byte strides below

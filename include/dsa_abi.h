@@ -65,9 +65,9 @@ extern "C" {
  * 64 and H a multiple of 16.  num_splits: 0 = automatic (fills the GPU),
  * otherwise the number of top-k chunks computed in parallel per token and
  * merged with log-sum-exp weights in a fixed order (results are
- * deterministic).  A chunk holds at most 2048 entries when H is a multiple of
- * 64 and 1024 otherwise, so longer rows always run split (the count is raised
- * to ceil(topk / that)); dsa_attn_num_splits() gives the count.  A split
+ * deterministic).  A chunk holds at most 2048 entries, so longer rows always
+ * run split (the count is raised to ceil(topk / 2048));
+ * dsa_attn_num_splits() gives the count.  A split
  * call needs dsa_attn_workspace_bytes() of workspace (16-byte aligned, contents
  * irrelevant) for the fp32 partials.
  *

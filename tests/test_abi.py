@@ -60,12 +60,12 @@ def test_abi_version_and_struct_layout(tmp_path):
 def test_split_choice():
     lib = _lib.load()
     assert lib.dsa_attn_num_splits(64, 16, 2048, 0) == 4       # decode fills 256 CUs
-    # a workgroup stages at most 1024 slot ids, so top-2048 rows take 2 chunks
-    assert lib.dsa_attn_num_splits(2048, 16, 2048, 0) == 2
+    # a workgroup takes chunks of up to 2048 keys
+    assert lib.dsa_attn_num_splits(2048, 16, 2048, 0) == 1     # 2048-key chunks: prefill needs no split
     assert lib.dsa_attn_num_splits(256, 128, 2048, 0) == 1     # one-slice layout: 2048-key chunks
     assert lib.dsa_attn_num_splits(64, 128, 4096, 1) == 2      # ... and no longer
     assert lib.dsa_attn_num_splits(2048, 16, 1024, 0) == 1     # prefill needs no split
-    assert lib.dsa_attn_num_splits(8, 16, 4096, 1) == 4        # requests below the minimum are raised
+    assert lib.dsa_attn_num_splits(8, 16, 4096, 1) == 2        # requests below the minimum are raised
     assert lib.dsa_attn_num_splits(1, 16, 2048, 0) == 16       # >= one tile per wave
     assert lib.dsa_attn_num_splits(64, 16, 2048, 16) == 16     # explicit request honoured
     assert lib.dsa_attn_num_splits(1, 16, 5, 128) == 5         # at most one key per split

@@ -138,6 +138,28 @@ def test_padding_anywhere_empty_rows_and_leading_pad_tile():
         assert torch.isfinite(out).all()
 
 
+@pytest.mark.parametrize("H,K", [(16, 2048), (16, 1500), (32, 2048), (32, 1100)])
+def test_one_chunk_past_the_slot_id_ring(H, K):
+    """One chunk per token longer than the 1024 slot ids the multi-slice
+    layouts keep in LDS: the ring is refilled half by half while the chunk
+    runs.  Padding, out-of-range ids and an all-padding tile past key 1024
+    must act as they do in the first 1024 keys."""
+    T = 5
+    d = workloads.attention_inputs(T, H, K, 128, 64, seed=H * 10000 + K)
+    g = d.pop("gen")
+    idx = torch.stack([torch.randperm(128 * 64, generator=g)[:K] for _ in range(T)]).to(torch.int32)
+    idx[1, 1024:1056] = -1                        # a whole refilled tile of padding
+    idx[2, 1030] = 128 * 64                       # out of range, past the ring
+    idx[2, 1700 % K] = -5
+    m = torch.rand(idx.shape, generator=g) < 0.2
+    idx[3][m[3]] = -1                             # padding everywhere
+    d.update(sparse_indices=idx, sm_scale=0.08)
+    clean = idx.clone()
+    clean[(clean < 0) | (clean >= 128 * 64)] = -1
+    out, lse = _run(kernel_splitk, d, SPLIT_K=1)
+    _assert_parity(out, lse, *_oracle(dict(d, sparse_indices=clean)), f"H={H} K={K} one chunk")
+
+
 def test_out_of_range_ids_are_padding():
     d = workloads.cfg2(T=4, seed=9)
     idx = d["sparse_indices"].clone()
