@@ -211,6 +211,20 @@ int prepare_attn(const char *fn, const dsa_attn_args *a, bool partial_only, dsa:
     p->ps_shift = sh;
     p->ps_magic = (uint32_t)(((uint64_t)1 << (31 + sh)) / (uint64_t)a->page_size + 1);
   }
+  {
+    // Narrow addressing: dense caches (a page is page_size consecutive rows,
+    // or pages of one row) whose extents stay below 2^31 bytes.
+    const int64_t ps = a->page_size;
+    const int64_t crs = ps == 1 ? p->ckv_sp : p->ckv_so, krs = ps == 1 ? p->kpe_sp : p->kpe_so;
+    const bool dense = ps == 1 || (p->ckv_sp == ps * p->ckv_so && p->kpe_sp == ps * p->kpe_so);
+    const int64_t n = p->num_slots;
+    p->narrow = dense && crs > 0 && krs > 0 && crs < (1 << 24) && krs < (1 << 24) &&
+                n < (1 << 24) && n * crs <= 0x7fffffffLL && n * krs <= 0x7fffffffLL;
+    p->ckv_rs = p->narrow ? (uint32_t)crs : 0;
+    p->kpe_rs = p->narrow ? (uint32_t)krs : 0;
+    p->ckv_extent = p->narrow ? (uint32_t)(n * crs) : 0;
+    p->kpe_extent = p->narrow ? (uint32_t)(n * krs) : 0;
+  }
   p->scale_log2 = a->sm_scale * 1.4426950408889634f;
   p->num_splits = S;
   p->chunk = chunk;

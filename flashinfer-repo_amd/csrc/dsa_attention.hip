@@ -21,7 +21,13 @@
 // gather; the page division is a multiply by a host-computed reciprocal) and
 // the valid-key mask of every tile is kept in one VGPR (lane i: tile i).
 // Padding keys gather a zero row, which keeps the number of loads per wave
-// and tile fixed and makes the vmcnt-based stage waits exact.
+// and tile fixed and makes the vmcnt-based stage waits exact.  Dense caches
+// below 2 GB (every BASELINE shape) are gathered with buffer_load ... lds at
+// 32-bit offsets slot * row stride (one 24-bit multiply per key, one readlane
+// per row); a padding key's offset lies past the buffer's range, and an
+// out-of-range buffer load returns zeros, which the DMA writes as the row.
+// Other caches take 64-bit addresses with the page arithmetic and a zero row
+// in global memory.
 //
 // Each wave belongs to one 16-head group and owns one slice of the 512 output
 // features.  Per tile:
@@ -135,10 +141,48 @@ __device__ __forceinline__ void lds_dma4(const void *gsrc, void *ldst) {
                                    (__attribute__((address_space(3))) void *)ldst, 4, 0, 0);
 }
 
-__device__ __forceinline__ bf16x4 lds_read_tr16(const char *p) {
-  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) i16x4 *)(p));
-  return __builtin_bit_cast(bf16x4, v);
+// V^T operands of four feature blocks F0 .. F0+3 with ds_read_b64_tr_b16: for
+// block f, keys 0-15 at vsrc + 32 f and keys 16-31 one 16-row block further
+// (ROWB bytes).  The eight reads and their lgkmcnt(0) wait are one asm
+// statement, so the compiler neither touches the destinations before the data
+// lands nor inserts the vmcnt(0) it puts in front of the builtin form (it
+// cannot tell the transpose read from an access to the LDS DMA targets).
+template <int F0, int ROWB>
+__device__ __forceinline__ void tr_read4(const char *vsrc, bf16x8 (&av)[4]) {
+  const uint32_t va = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)vsrc;
+  u32x2 a0, a1, a2, a3, b0, b1, b2, b3;
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %8 offset:%9\n\t"
+      "ds_read_b64_tr_b16 %4, %8 offset:%13\n\t"
+      "ds_read_b64_tr_b16 %1, %8 offset:%10\n\t"
+      "ds_read_b64_tr_b16 %5, %8 offset:%14\n\t"
+      "ds_read_b64_tr_b16 %2, %8 offset:%11\n\t"
+      "ds_read_b64_tr_b16 %6, %8 offset:%15\n\t"
+      "ds_read_b64_tr_b16 %3, %8 offset:%12\n\t"
+      "ds_read_b64_tr_b16 %7, %8 offset:%16\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(a0), "=&v"(a1), "=&v"(a2), "=&v"(a3), "=&v"(b0), "=&v"(b1), "=&v"(b2), "=&v"(b3)
+      : "v"(va), "i"(F0 * 32), "i"(F0 * 32 + 32), "i"(F0 * 32 + 64), "i"(F0 * 32 + 96),
+        "i"(ROWB + F0 * 32), "i"(ROWB + F0 * 32 + 32), "i"(ROWB + F0 * 32 + 64),
+        "i"(ROWB + F0 * 32 + 96)
+      : "memory");
+  av[0] = __builtin_bit_cast(bf16x8, (u32x4){a0[0], a0[1], b0[0], b0[1]});
+  av[1] = __builtin_bit_cast(bf16x8, (u32x4){a1[0], a1[1], b1[0], b1[1]});
+  av[2] = __builtin_bit_cast(bf16x8, (u32x4){a2[0], a2[1], b2[0], b2[1]});
+  av[3] = __builtin_bit_cast(bf16x8, (u32x4){a3[0], a3[1], b3[0], b3[1]});
+}
+
+// tr_read4 for every feature block of a wave's slice, four at a time, each
+// batch followed by its MFMAs (fn(f0, av)).
+template <int NFB, int ROWB, int F0 = 0, typename Fn>
+__device__ __forceinline__ void for_tr_batches(const char *vsrc, Fn &&fn) {
+  static_assert(NFB % 4 == 0, "feature blocks come in batches of four");
+  if constexpr (F0 < NFB) {
+    bf16x8 av[4];
+    tr_read4<F0, ROWB>(vsrc, av);
+    fn(F0, av);
+    for_tr_batches<NFB, ROWB, F0 + 4>(vsrc, fn);
+  }
 }
 
 __device__ __forceinline__ uint64_t readlane64(uint64_t v, int lane) {
@@ -218,7 +262,10 @@ struct Ring {
   static_assert(FS == 1 || FS == 2 || FS == 4 || FS == 8, "feature slices");
 };
 
-template <int W, int FS>
+// NARROW: the caches are dense (slot s at byte s * row stride) and below
+// 2 GB, so the gathers address them with 32-bit offsets through buffer
+// resources; otherwise through 64-bit addresses with the page arithmetic.
+template <int W, int FS, bool NARROW>
 __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) {
   using R = Ring<W, FS>;
   using L = Lds<FS>;
@@ -295,35 +342,61 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
   // (8 rows) this wave gathers (a half group when W == 8).
   const int grp = (W == 4) ? wave : (wave >> 1);
   const int row0 = (W == 4) ? 0 : 4 * (wave & 1);  // first ckv row within the group
-  const uint64_t zero_row = (uint64_t)(const char *)g_zero_row;
   // valid-key mask of tile i in lane i (wave-uniform reads with readlane):
   // tiles of the first ring pass are masked after the first gathers are
   // issued, tiles of refilled ids when they are issued
   uint32_t tile_masks = 0;
+  const bool kpe_lane = W == 4 || (lane >> 5) == (wave & 1);  // this lane's kpe chunk is gathered here
+  auto note_refilled_mask = [&](int j, const int32_t *ids) {
+    if (FS >= 2 && j >= L::kRingTiles) {
+      const uint32_t id = (uint32_t)ids[lane & 31];
+      const uint32_t bits = (uint32_t)__ballot(id < (uint32_t)p.num_slots);
+      tile_masks = lane == j ? bits : tile_masks;
+    }
+  };
+  // NARROW: one 32-bit byte offset per key (slot * row stride); a padding or
+  // out-of-range key gets kOOB, past the end of every buffer, and a buffer
+  // load beyond its range returns zeros, so its row lands as zeros.
+  constexpr uint32_t kOOB = 0x80000000u;
+  const auto ckv_rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)p.ckv, 0, (int)p.ckv_extent, kBufferFlags);
+  const auto kpe_rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)p.kpe, 0, (int)p.kpe_extent, kBufferFlags);
   auto issue_tile = [&](int j) {
     char *st = lds + (j % kStages) * kStageBytes;
     const int32_t *ids = slots + (j % L::kRingTiles) * kKeysPerTile;  // refilled ids are raw
-    const int sl = ids[grp * 8 + (lane & 7)];
-    if (FS >= 2 && j >= L::kRingTiles) {
-      const int id = ids[lane & 31];
-      const uint32_t bits = (uint32_t)__ballot(id >= 0 && (int64_t)id < p.num_slots);
-      tile_masks = lane == j ? bits : tile_masks;
-    }
-    uint64_t ckv_addr = zero_row, kpe_addr = zero_row;
-    if (sl >= 0 && (int64_t)sl < p.num_slots) {
-      const uint32_t pg = (uint32_t)(((uint64_t)(uint32_t)sl * p.ps_magic) >> (31 + p.ps_shift));
-      const uint32_t of = (uint32_t)sl - pg * (uint32_t)p.page_size;
-      ckv_addr = (uint64_t)(p.ckv + (int64_t)pg * p.ckv_sp + (int64_t)of * p.ckv_so);
-      kpe_addr = (uint64_t)(p.kpe + (int64_t)pg * p.kpe_sp + (int64_t)of * p.kpe_so);
-    }
-#pragma unroll
-    for (int m = 0; m < R::kRows; ++m) {
-      const char *src = (const char *)readlane64(ckv_addr, row0 + m) + lane * 16;
-      lds_dma16(src, st + (grp * 8 + row0 + m) * kCkvPitch);
-    }
+    note_refilled_mask(j, ids);
     char *kdst = st + kCkvStageBytes + grp * kKpeGroupPitch;
-    const char *ksrc = (const char *)kpe_addr + (lane >> 3) * 16;
-    if (W == 4 || (lane >> 5) == (wave & 1)) lds_dma16(ksrc, kdst);
+    if constexpr (NARROW) {
+      const uint32_t sl = (uint32_t)ids[grp * 8 + (lane & 7)];
+      const bool ok = sl < (uint32_t)p.num_slots;  // -1 wraps to 2^32 - 1
+      const uint32_t co = ok ? __umul24(sl, p.ckv_rs) : kOOB;
+      const uint32_t ko = ok ? __umul24(sl, p.kpe_rs) : kOOB;
+#pragma unroll
+      for (int m = 0; m < R::kRows; ++m) {
+        const uint32_t ro = __builtin_amdgcn_readlane(co, row0 + m);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            ckv_rsrc, (__attribute__((address_space(3))) void *)(st + (grp * 8 + row0 + m) * kCkvPitch),
+            16, ro + lane * 16, 0, 0, 0);
+      }
+      if (kpe_lane)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(kpe_rsrc, (__attribute__((address_space(3))) void *)kdst,
+                                                 16, ko + (lane >> 3) * 16, 0, 0, 0);
+    } else {
+      const int sl = ids[grp * 8 + (lane & 7)];
+      const uint64_t zero_row = (uint64_t)(const char *)g_zero_row;
+      uint64_t ckv_addr = zero_row, kpe_addr = zero_row;
+      if (sl >= 0 && (int64_t)sl < p.num_slots) {
+        const uint32_t pg = (uint32_t)(((uint64_t)(uint32_t)sl * p.ps_magic) >> (31 + p.ps_shift));
+        const uint32_t of = (uint32_t)sl - pg * (uint32_t)p.page_size;
+        ckv_addr = (uint64_t)(p.ckv + (int64_t)pg * p.ckv_sp + (int64_t)of * p.ckv_so);
+        kpe_addr = (uint64_t)(p.kpe + (int64_t)pg * p.kpe_sp + (int64_t)of * p.kpe_so);
+      }
+#pragma unroll
+      for (int m = 0; m < R::kRows; ++m) {
+        const char *src = (const char *)readlane64(ckv_addr, row0 + m) + lane * 16;
+        lds_dma16(src, st + (grp * 8 + row0 + m) * kCkvPitch);
+      }
+      if (kpe_lane) lds_dma16((const char *)kpe_addr + (lane >> 3) * 16, kdst);
+    }
   };
 
   f32x4 acc[R::kNFB];
@@ -522,15 +595,16 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
     // 64 of them) ahead of the MFMAs.
     const char *vsrc = st_ckv + (kbase + 2 * (r16 >> 2)) * kCkvPitch +
                        (fs * R::kNFB * 16 + 4 * (r16 & 3)) * 2;
+    // The reads are tr_read4 batches (inline asm): with the builtin form the
+    // compiler waits for every outstanding LDS DMA (vmcnt(0)) before the
+    // first read, which drains the gathers in flight on every tile.
+    for_tr_batches<R::kNFB, 16 * kCkvPitch>(vsrc, [&](int f0, const bf16x8(&av)[4]) {
 #pragma unroll
-    for (int fb = 0; fb < R::kNFB; ++fb) {
-      const bf16x4 lo4 = lds_read_tr16(vsrc + fb * 32);
-      const bf16x4 hi4 = lds_read_tr16(vsrc + 16 * kCkvPitch + fb * 32);
-      const bf16x8 av = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
-      const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, p_hi, acc[fb], 0, 0, 0);
-      acc[fb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, p_lo, c, 0, 0, 0);
-      if (R::kNFB > 8 && fb % 4 == 3) __builtin_amdgcn_sched_barrier(0);
-    }
+      for (int f = 0; f < 4; ++f) {
+        const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[f], p_hi, acc[f0 + f], 0, 0, 0);
+        acc[f0 + f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[f], p_lo, c, 0, 0, 0);
+      }
+    });
   };
 
   const int pre = min(n_tiles, kStages - 1);
@@ -826,8 +900,11 @@ __global__ __launch_bounds__(128) void dsa_attn_combine_kernel(AttnParams p) {
 
 template <int W, int FS>
 hipError_t launch_ring(const AttnParams &p, int head_blocks, hipStream_t stream) {
-  hipLaunchKernelGGL((dsa_attn_ring_kernel<W, FS>), dim3(p.T * p.num_splits, head_blocks),
-                     dim3(W * 64), 0, stream, p);
+  const dim3 grid(p.T * p.num_splits, head_blocks), block(W * 64);
+  if (p.narrow)
+    hipLaunchKernelGGL((dsa_attn_ring_kernel<W, FS, true>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((dsa_attn_ring_kernel<W, FS, false>), grid, block, 0, stream, p);
   return hipGetLastError();
 }
 

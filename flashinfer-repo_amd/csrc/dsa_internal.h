@@ -55,6 +55,12 @@ struct AttnParams {
   // [T][head blocks][8], zero before the launch and left zero by it.  Null:
   // the separate merge kernel runs.
   uint32_t *counters;
+  // Narrow addressing (set when the host has checked it applies): slot s's
+  // rows sit at byte s * ckv_rs / s * kpe_rs of their caches, every such
+  // offset of a valid slot lies below ckv_extent / kpe_extent <= 2^31, and
+  // ckv_rs, kpe_rs and the slot count are below 2^24 (24-bit multiplies).
+  int32_t narrow;
+  uint32_t ckv_rs, kpe_rs, ckv_extent, kpe_extent;
 };
 
 // Counter words a split call with in-kernel merge uses.
