@@ -287,7 +287,8 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
   const int qb0 = FS >= 2 ? (fs & 1) : 0;
   const int part = FS >= 2 ? (fs >> 1) : 0;
 
-  // the 8-slice layout shares the softmax work through LDS (softmax_shared)
+  // the 8-slice layout shares the softmax work through LDS (softmax_publish /
+  // consume_words)
   constexpr bool kShared = W == 8 && FS == 8;
   const int k_begin = split * p.chunk;
   const int n_keys = max(0, min(p.K, k_begin + p.chunk) - k_begin);
@@ -419,7 +420,7 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
     }
   };
   // Partial S^T exchange: slot w holds wave w's partial of its key block.
-  // The 8-slice layout reads single components (softmax_shared), so it keeps
+  // The 8-slice layout reads single components (value_logit), so it keeps
   // them component-major (each read is 64 consecutive words, no bank
   // conflicts); the others read whole f32x4 per lane.
   auto xput = [&](const f32x4 &v) {
@@ -523,28 +524,40 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
     return (uint32_t *)(lds + (c >> 2) * kStageBytes + kCkvStageBytes + (c & 3) * kKpeGroupPitch +
                         1024 + (l & 31) * 4);
   };
-  auto softmax_shared = [&](uint32_t vmask, bf16x8 &p_hi, bf16x8 &p_lo) {
-    const int v = wave, b = v >> 2, k = v & 3;
-    const float c = p.scale_log2;
-    // this lane's score of value v: the partials added in the order reduce() uses
+  // The words of tile i are published after the partial exchange of
+  // iteration i and read after the first barrier of iteration i + 1 (which
+  // also finds tile i + 1 landed), one barrier per tile for both.  This
+  // wave's value waits in pv_pending until the words show whether the tile
+  // overshot the reference max.
+  float pv_pending = 0.f;
+  auto publish = [&](float d, bool flag) {
+    const float pv = fast_exp2(d);
+    const __bf16 hi = (__bf16)pv;
+    const __bf16 lo = (__bf16)(pv - (float)hi);
+    const uint32_t w = ((uint32_t)__builtin_bit_cast(uint16_t, hi) | (flag ? 0x8000u : 0u)) << 16 |
+                       (uint32_t)__builtin_bit_cast(uint16_t, lo);
+    *pword(wave, lane) = w;
+    pv_pending = pv;
+  };
+  // this lane's score of value v = wave (head r16, key b*16 + kbase + 2k):
+  // the partials added in the order reduce() uses; -inf when masked
+  auto value_logit = [&](uint32_t vmask) -> float {
+    const int b = wave >> 2, k = wave & 3;
     const float *x = (const float *)xbuf;
     float sc = x[(b * 4 + k) * 64 + lane];
 #pragma unroll
     for (int pp = 1; pp < R::kParts; ++pp) sc += x[((b + 2 * pp) * 4 + k) * 64 + lane];
     const bool valid = ((vmask >> (b * 16 + kbase + 2 * k)) & 1u) != 0;
-    auto publish = [&](float d, bool flag) {
-      const float pv = fast_exp2(d);
-      const __bf16 hi = (__bf16)pv;
-      const __bf16 lo = (__bf16)(pv - (float)hi);
-      const uint32_t w = ((uint32_t)__builtin_bit_cast(uint16_t, hi) | (flag ? 0x8000u : 0u)) << 16 |
-                         (uint32_t)__builtin_bit_cast(uint16_t, lo);
-      *pword(v, lane) = w;
-      return pv;
-    };
-    float d = valid ? __builtin_fmaf(sc, c, -m_run) : -INFINITY;
-    float pv = publish(d, d > kRescaleSlack);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
+    return valid ? __builtin_fmaf(sc, p.scale_log2, -m_run) : -INFINITY;
+  };
+  auto softmax_publish = [&](uint32_t vmask) {
+    const float d = value_logit(vmask);
+    publish(d, d > kRescaleSlack);
+  };
+  // Reads the 512 words of a tile whose partial scores are still in xbuf;
+  // if any overshoots, moves the reference max to the tile's max, rescales
+  // and republishes (every wave reads the same words, so all take the branch).
+  auto consume_words = [&](uint32_t vmask, bf16x8 &p_hi, bf16x8 &p_lo) {
     uint32_t w[8];
     uint32_t flags = 0;
 #pragma unroll
@@ -552,10 +565,11 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
       w[j] = *pword(j, lane);
       flags |= w[j];
     }
-    if (__ballot((flags >> 31) != 0) != 0) {  // uniform: every wave read the same 512 words
-      __builtin_amdgcn_s_barrier();           // all flags read before any word is rewritten
+    if (__ballot((flags >> 31) != 0) != 0) {
+      __builtin_amdgcn_s_barrier();  // all flags read before any word is rewritten
       f32x4 sacc[2];
       reduce(sacc);
+      const float c = p.scale_log2;
       const uint32_t vm = vmask >> kbase;
       float mx = -INFINITY;
 #pragma unroll
@@ -571,17 +585,17 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
       l_run *= alpha;
 #pragma unroll
       for (int fb = 0; fb < R::kNFB; ++fb) acc[fb] *= alpha;
-      d = valid ? __builtin_fmaf(sc, c, -m_run) : -INFINITY;
-      pv = publish(d, false);
-      __builtin_amdgcn_s_waitcnt(0xC07F);
-      __builtin_amdgcn_s_barrier();
+      publish(value_logit(vmask), false);
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      __builtin_amdgcn_s_barrier();        // republished words visible, xbuf reads done
 #pragma unroll
       for (int j = 0; j < 8; ++j) w[j] = *pword(j, lane);
     }
-    l_run += pv;  // this wave's share; the shares are added at the end
+    l_run += pv_pending;  // this wave's share; the shares are added at the end
+    // no word carries a flag here (none was set, or all were republished)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      p_hi[j] = __builtin_bit_cast(__bf16, (uint16_t)((w[j] >> 16) & 0x7fffu));
+      p_hi[j] = __builtin_bit_cast(__bf16, (uint16_t)(w[j] >> 16));
       p_lo[j] = __builtin_bit_cast(__bf16, (uint16_t)(w[j] & 0xffffu));
     }
   };
@@ -640,7 +654,10 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
   bf16x8 p_hi = {}, p_lo = {};
   for (int i = 0; i < n_tiles; ++i) {
     wait_tile(i);
-    __builtin_amdgcn_s_barrier();  // every wave's share of tile i landed
+    if constexpr (kShared) __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's words of tile i-1 written
+    __builtin_amdgcn_s_barrier();  // every wave's share of tile i landed (and tile i-1's words)
+    if constexpr (kShared)
+      if (i > 0) consume_words(__builtin_amdgcn_readlane(tile_masks, i - 1), p_hi, p_lo);
     const char *st_ckv = lds + (i % kStages) * kStageBytes;
     f32x4 sacc[2];
     scores(st_ckv, sacc);
@@ -668,13 +685,20 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
       }
     }
     if constexpr (kShared) {
-      softmax_shared(__builtin_amdgcn_readlane(tile_masks, i), p_hi, p_lo);
+      softmax_publish(__builtin_amdgcn_readlane(tile_masks, i));
     } else {
       if (FS >= 2) reduce(sacc);
       softmax(sacc, __builtin_amdgcn_readlane(tile_masks, i), p_hi, p_lo);
     }
   }
-  if (n_tiles > 0) pv(lds + ((n_tiles - 1) % kStages) * kStageBytes, p_hi, p_lo);
+  if (n_tiles > 0) {
+    if constexpr (kShared) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      __builtin_amdgcn_s_barrier();  // the last tile's words visible
+      consume_words(__builtin_amdgcn_readlane(tile_masks, n_tiles - 1), p_hi, p_lo);
+    }
+    pv(lds + ((n_tiles - 1) % kStages) * kStageBytes, p_hi, p_lo);
+  }
 
   // ---- epilogue: lanes of a head hold partial sums over disjoint keys (and,
   // with the probability exchange, each wave over its share of the values)
