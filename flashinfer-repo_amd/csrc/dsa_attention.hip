@@ -135,6 +135,13 @@ __device__ __forceinline__ void lds_dma16(const void *gsrc, void *ldst) {
                                    (__attribute__((address_space(3))) void *)ldst, 16, 0, 0);
 }
 
+// 16 bytes per lane from a buffer resource at byte offset voff (lane i lands
+// at ldst + 16 i; an offset past the resource's range lands zeros).
+__device__ __forceinline__ void lds_dma16_buf(__amdgpu_buffer_rsrc_t rsrc, void *ldst, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)ldst, 16,
+                                           voff, 0, 0, 0);
+}
+
 // 4 bytes per lane: lane i lands at ldst + 4 i.
 __device__ __forceinline__ void lds_dma4(const void *gsrc, void *ldst) {
   __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)gsrc,
@@ -211,14 +218,18 @@ __device__ __forceinline__ void wait_vmcnt() {
 template <int S0, int N>
 __device__ __forceinline__ f32x4 qk_steps(const char *rowp, const char *kp, const bf16x8 *q,
                                           int g) {
-  f32x4 c = {0.f, 0.f, 0.f, 0.f};
+  // Short ranges (waves that split the steps) use two independent accumulator
+  // chains, even and odd steps, added at the end; the full 18-step range of the
+  // one-slice layouts keeps one chain (its waves have no VGPRs to spare).
+  constexpr int kChains = (N > 1 && N < 18) ? 2 : 1;
+  f32x4 c[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
   for (int k = 0; k < N; ++k) {
     const int s = S0 + k;
     const char *ap = s < 16 ? rowp + s * 64 : kp + ((s - 16) * 4 + g) * 128;
-    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)ap, q[k], c, 0, 0, 0);
+    c[k % kChains] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)ap, q[k], c[k % kChains], 0, 0, 0);
   }
-  return c;
+  return kChains == 2 ? c[0] + c[1] : c[0];
 }
 
 // k-step range [first(P), first(P+1)) of part P when 18 steps are cut into NP.
@@ -245,6 +256,14 @@ __device__ __forceinline__ f32x4 qk_part(int part, const char *rowp, const char 
     default: return qk_steps<P::first(3), P::count(3)>(rowp, kp, q, g);
   }
 }
+
+// Source of one wave's share of a tile gather (see tile_src in the kernel).
+template <int ROWS>
+struct GatherSrc {
+  uint32_t row[ROWS];  // narrow: ckv byte offset of each row this wave gathers
+  uint32_t ko;         // narrow: kpe byte offset of this lane's 16-byte chunk
+  uint64_t ckv, kpe;   // otherwise: row addresses of this lane's key
+};
 
 // W waves per workgroup; FS waves share one 16-head group, each owning
 // 512/FS output features.  W/FS head groups per workgroup.  With FS > 1 the
@@ -361,42 +380,49 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
   constexpr uint32_t kOOB = 0x80000000u;
   const auto ckv_rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)p.ckv, 0, (int)p.ckv_extent, kBufferFlags);
   const auto kpe_rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)p.kpe, 0, (int)p.kpe_extent, kBufferFlags);
-  auto issue_tile = [&](int j) {
-    char *st = lds + (j % kStages) * kStageBytes;
+  // A tile's gather in two steps: tile_src reads the slot ids and computes the
+  // row addresses (LDS reads and arithmetic, done before the barrier that
+  // frees the stage, off the path between the barriers); fire_tile issues the
+  // DMAs into stage j % kStages.
+  using TileSrc = GatherSrc<R::kRows>;
+  auto tile_src = [&](int j) {
+    TileSrc a;
     const int32_t *ids = slots + (j % L::kRingTiles) * kKeysPerTile;  // refilled ids are raw
     note_refilled_mask(j, ids);
-    char *kdst = st + kCkvStageBytes + grp * kKpeGroupPitch;
     if constexpr (NARROW) {
       const uint32_t sl = (uint32_t)ids[grp * 8 + (lane & 7)];
       const bool ok = sl < (uint32_t)p.num_slots;  // -1 wraps to 2^32 - 1
       const uint32_t co = ok ? __umul24(sl, p.ckv_rs) : kOOB;
-      const uint32_t ko = ok ? __umul24(sl, p.kpe_rs) : kOOB;
 #pragma unroll
-      for (int m = 0; m < R::kRows; ++m) {
-        const uint32_t ro = __builtin_amdgcn_readlane(co, row0 + m);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            ckv_rsrc, (__attribute__((address_space(3))) void *)(st + (grp * 8 + row0 + m) * kCkvPitch),
-            16, ro + lane * 16, 0, 0, 0);
-      }
-      if (kpe_lane)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(kpe_rsrc, (__attribute__((address_space(3))) void *)kdst,
-                                                 16, ko + (lane >> 3) * 16, 0, 0, 0);
+      for (int m = 0; m < R::kRows; ++m) a.row[m] = __builtin_amdgcn_readlane(co, row0 + m);
+      a.ko = (ok ? __umul24(sl, p.kpe_rs) : kOOB) + (lane >> 3) * 16;
     } else {
       const int sl = ids[grp * 8 + (lane & 7)];
-      const uint64_t zero_row = (uint64_t)(const char *)g_zero_row;
-      uint64_t ckv_addr = zero_row, kpe_addr = zero_row;
+      a.ckv = a.kpe = (uint64_t)(const char *)g_zero_row;
       if (sl >= 0 && (int64_t)sl < p.num_slots) {
         const uint32_t pg = (uint32_t)(((uint64_t)(uint32_t)sl * p.ps_magic) >> (31 + p.ps_shift));
         const uint32_t of = (uint32_t)sl - pg * (uint32_t)p.page_size;
-        ckv_addr = (uint64_t)(p.ckv + (int64_t)pg * p.ckv_sp + (int64_t)of * p.ckv_so);
-        kpe_addr = (uint64_t)(p.kpe + (int64_t)pg * p.kpe_sp + (int64_t)of * p.kpe_so);
+        a.ckv = (uint64_t)(p.ckv + (int64_t)pg * p.ckv_sp + (int64_t)of * p.ckv_so);
+        a.kpe = (uint64_t)(p.kpe + (int64_t)pg * p.kpe_sp + (int64_t)of * p.kpe_so);
       }
+    }
+    return a;
+  };
+  auto fire_tile = [&](int j, const TileSrc &a) {
+    char *st = lds + (j % kStages) * kStageBytes;
+    char *kdst = st + kCkvStageBytes + grp * kKpeGroupPitch;
+    if constexpr (NARROW) {
+#pragma unroll
+      for (int m = 0; m < R::kRows; ++m)
+        lds_dma16_buf(ckv_rsrc, st + (grp * 8 + row0 + m) * kCkvPitch, a.row[m] + lane * 16);
+      if (kpe_lane) lds_dma16_buf(kpe_rsrc, kdst, a.ko);
+    } else {
 #pragma unroll
       for (int m = 0; m < R::kRows; ++m) {
-        const char *src = (const char *)readlane64(ckv_addr, row0 + m) + lane * 16;
+        const char *src = (const char *)readlane64(a.ckv, row0 + m) + lane * 16;
         lds_dma16(src, st + (grp * 8 + row0 + m) * kCkvPitch);
       }
-      if (kpe_lane) lds_dma16((const char *)kpe_addr + (lane >> 3) * 16, kdst);
+      if (kpe_lane) lds_dma16((const char *)a.kpe + (lane >> 3) * 16, kdst);
     }
   };
 
@@ -622,7 +648,7 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
   };
 
   const int pre = min(n_tiles, kStages - 1);
-  for (int j = 0; j < pre; ++j) issue_tile(j);
+  for (int j = 0; j < pre; ++j) fire_tile(j, tile_src(j));
 
   // the first ring pass's tile masks, built while the first tiles are in flight
   for (int k = 0; 2 * k < min(n_tiles, L::kRingTiles); ++k) {
@@ -663,9 +689,15 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
     scores(st_ckv, sacc);
     if (i > 0) pv(lds + ((i - 1) % kStages) * kStageBytes, p_hi, p_lo);
     if (FS >= 2) xput(sacc[0]);
+    // (The one-slice layouts compute the addresses after the barrier: their
+    // waves have no registers to hold them across it.)
+    const bool refill_stage = i + kStages - 1 < n_tiles;
+    TileSrc nxt;
+    if (FS >= 2 && refill_stage) nxt = tile_src(i + kStages - 1);
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): partial written, tile i-1 read
     __builtin_amdgcn_s_barrier();
-    if (i + kStages - 1 < n_tiles) issue_tile(i + kStages - 1);
+    if (FS == 1 && refill_stage) nxt = tile_src(i + kStages - 1);
+    if (refill_stage) fire_tile(i + kStages - 1, nxt);
     // Ring refill (layouts whose ring holds 32 tiles' ids): once tile J = 16 m
     // (m >= 1) is issued, every wave has passed a barrier since it read the
     // ids of tiles J - 16 .. J - 1, so their half of the ring takes the ids of
