@@ -213,48 +213,55 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// Partial S^T over k-steps S0..S0+N-1 (step s < 16: ckv features 32s..;
-// s = 16, 17: kpe) for this lane's key row rowp / kpe chunk base kp.
-template <int S0, int N>
-__device__ __forceinline__ f32x4 qk_steps(const char *rowp, const char *kp, const bf16x8 *q,
-                                          int g) {
-  // Short ranges (waves that split the steps) use two independent accumulator
-  // chains, even and odd steps, added at the end; the full 18-step range of the
-  // one-slice layouts keeps one chain (its waves have no VGPRs to spare).
-  constexpr int kChains = (N > 1 && N < 18) ? 2 : 1;
-  f32x4 c[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-  for (int k = 0; k < N; ++k) {
-    const int s = S0 + k;
-    const char *ap = s < 16 ? rowp + s * 64 : kp + ((s - 16) * 4 + g) * 128;
-    c[k % kChains] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)ap, q[k], c[k % kChains], 0, 0, 0);
-  }
-  return kChains == 2 ? c[0] + c[1] : c[0];
-}
-
-// k-step range [first(P), first(P+1)) of part P when 18 steps are cut into NP.
+// QK split among the NP waves that share a key block: part p takes the
+// 32-feature nope steps [16p/NP, 16(p+1)/NP) and the kpe features
+// [64p/NP, 64(p+1)/NP) -- NP = 1: 16 nope + two 32-feature kpe steps; NP = 2:
+// 8 + one; NP = 4: 4 nope steps + one 16-feature kpe step (the 16x16x16 MFMA).
+// Every part has the same shape, so a wave's range is an address offset.
 template <int NP>
-struct Parts {
-  static constexpr int first(int part) { return part * 18 / NP; }
-  static constexpr int count(int part) { return first(part + 1) - first(part); }
-  static constexpr int kMax = (18 + NP - 1) / NP;
+struct QkSplit {
+  static_assert(NP == 1 || NP == 2 || NP == 4, "parts per key block");
+  static constexpr int kNope = 16 / NP;               // 32-feature nope steps per part
+  static constexpr int kPe32 = NP <= 2 ? 2 / NP : 0;  // 32-feature kpe steps per part
+  static constexpr bool kPe16 = NP == 4;              // one 16-feature kpe step
 };
 
+// Q^T operands (the B side of S^T = K Q^T) of one part, this lane's k-slots.
+template <int NP>
+struct QkOperands {
+  bf16x8 nope[QkSplit<NP>::kNope];
+  bf16x8 pe32[QkSplit<NP>::kPe32 > 0 ? QkSplit<NP>::kPe32 : 1];
+  i16x4 pe16;
+};
+
+// Partial S^T of part `part` for this lane's key: rowp = its ckv row in LDS
+// (+ 16 g), kp = its kpe row's first chunk (kpe rows are chunk-major: chunk c
+// of row r at (8c + r) * 16 within the 8-row group).  Split parts keep two
+// independent MFMA chains added at the end; the full range of the one-slice
+// layouts keeps one chain (its waves have no registers to spare).
 template <int NP>
 __device__ __forceinline__ f32x4 qk_part(int part, const char *rowp, const char *kp,
-                                         const bf16x8 *q, int g) {
-  using P = Parts<NP>;
-  if (NP == 1) return qk_steps<0, 18>(rowp, kp, q, g);
-  if (NP == 2) {
-    if (part == 0) return qk_steps<0, P::count(0)>(rowp, kp, q, g);
-    return qk_steps<P::first(1), P::count(1)>(rowp, kp, q, g);
+                                         const QkOperands<NP> &q, int g) {
+  using Q = QkSplit<NP>;
+  constexpr int kChains = NP > 1 ? 2 : 1;
+  f32x4 c[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  const char *np = rowp + part * (Q::kNope * 64);
+#pragma unroll
+  for (int k = 0; k < Q::kNope; ++k)
+    c[k % kChains] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8 *)(np + k * 64),
+                                                             q.nope[k], c[k % kChains], 0, 0, 0);
+#pragma unroll
+  for (int j = 0; j < Q::kPe32; ++j) {
+    const int step = part * Q::kPe32 + j;  // 32 kpe features = chunks 4 step .. 4 step + 3
+    c[(Q::kNope + j) % kChains] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+        *(const bf16x8 *)(kp + (step * 4 + g) * 128), q.pe32[j], c[(Q::kNope + j) % kChains], 0, 0, 0);
   }
-  switch (part) {
-    case 0: return qk_steps<0, P::count(0)>(rowp, kp, q, g);
-    case 1: return qk_steps<P::first(1), P::count(1)>(rowp, kp, q, g);
-    case 2: return qk_steps<P::first(2), P::count(2)>(rowp, kp, q, g);
-    default: return qk_steps<P::first(3), P::count(3)>(rowp, kp, q, g);
+  if constexpr (Q::kPe16) {
+    // features 16 part + 4g .. +3: chunk 2 part + g/2, bytes (g & 1) * 8 of it
+    const i16x4 a = *(const i16x4 *)(kp + (2 * part + (g >> 1)) * 128 + (g & 1) * 8);
+    c[1] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, q.pe16, c[1], 0, 0, 0);
   }
+  return kChains == 2 ? c[0] + c[1] : c[0];
 }
 
 // Source of one wave's share of a tile gather (see tile_src in the kernel).
@@ -276,7 +283,6 @@ struct Ring {
   static constexpr int kLoads = kRows + 1;        // + one kpe DMA (full or half)
   static constexpr int kParts = FS >= 2 ? FS / 2 : 1;  // k-step ranges per key block
   static constexpr int kBlocks = FS >= 2 ? 1 : 2;      // key blocks one wave computes
-  static constexpr int kQRegs = Parts<kParts>::kMax;   // Q operand registers (x4 VGPRs)
   static_assert(W == 4 || W == 8, "gather split assumes 4 or 8 waves");
   static_assert(FS == 1 || FS == 2 || FS == 4 || FS == 8, "feature slices");
 };
@@ -313,21 +319,21 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
   const int n_keys = max(0, min(p.K, k_begin + p.chunk) - k_begin);
   const int n_tiles = (n_keys + kKeysPerTile - 1) / kKeysPerTile;
 
-  // Q^T as the B operand of S^T = K Q^T: k-step s covers features 32s..32s+31
-  // (s < 16: q_nope; s = 16, 17: q_pe); this lane holds 8g..8g+7 of them.
+  // Q^T as the B operand of S^T = K Q^T (QkSplit: this wave's part of the
+  // 576 features; per 32-feature step the lane holds features 8g..8g+7).
   // Issued before the slot-id staging, whose LDS stores wait for the index
   // loads: both loads are then in flight together (one memory latency).
-  bf16x8 qreg[R::kQRegs];
+  QkOperands<R::kParts> qreg;
   {
-    const int s0 = Parts<R::kParts>::first(part);
-    const int ns = Parts<R::kParts>::first(part + 1) - s0;
-    const char *qn = p.q_nope + t * p.qn_st + head * p.qn_sh + g * 16;
-    const char *qp = p.q_pe + t * p.qp_st + head * p.qp_sh + g * 16;
+    using Q = QkSplit<R::kParts>;
+    const char *qn = p.q_nope + t * p.qn_st + head * p.qn_sh + g * 16 + part * (Q::kNope * 64);
+    const char *qp = p.q_pe + t * p.qp_st + head * p.qp_sh;
 #pragma unroll
-    for (int k = 0; k < R::kQRegs; ++k) {
-      const int s = s0 + k;
-      if (k < ns) qreg[k] = *(const bf16x8 *)(s < 16 ? qn + s * 64 : qp + (s - 16) * 64);
-    }
+    for (int k = 0; k < Q::kNope; ++k) qreg.nope[k] = *(const bf16x8 *)(qn + k * 64);
+#pragma unroll
+    for (int j = 0; j < Q::kPe32; ++j)
+      qreg.pe32[j] = *(const bf16x8 *)(qp + (part * Q::kPe32 + j) * 64 + g * 16);
+    if constexpr (Q::kPe16) qreg.pe16 = *(const i16x4 *)(qp + part * 32 + g * 8);
   }
   // ---- stage the slot ids of the chunk's first kRingTiles tiles (padding and
   // out-of-range ids -> -1); all index loads are issued before the first
