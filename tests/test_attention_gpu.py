@@ -224,6 +224,41 @@ def test_page_sizes_not_powers_of_two_and_padded_pages():
     assert torch.equal(out.cpu(), out_ref) and torch.equal(lse.cpu(), lse_ref), "padded pages"
 
 
+@pytest.mark.parametrize("num_pages", [32767, 33024])
+def test_caches_near_and_beyond_2gb(num_pages):
+    """A dense cache whose ckv extent stays below 2^31 bytes is gathered at
+    32-bit buffer offsets (32767 pages of 64 rows: the last row ends 64 KB
+    below 2 GB); a larger one at 64-bit addresses (33024 pages, 2.16 GB).  The
+    selected rows are written into an otherwise uninitialised cache, so a
+    gather of any other row would show; both must match the oracle on a
+    compact copy of the selected rows."""
+    g = torch.Generator().manual_seed(31)
+    T, H, K, ps = 4, 16, 600, 64
+    slots = num_pages * ps
+    pick = torch.cat([torch.randperm(slots - 1, generator=g)[:T * K - 1],
+                      torch.tensor([slots - 1])])  # distinct, the last slot included
+    order = torch.randperm(T * K, generator=g)
+    idx = pick[order].reshape(T, K).to(torch.int32)
+    idx[2, 500:] = -1
+    rows_ckv = (torch.randn(T * K, 512, generator=g) * 0.7).to(torch.bfloat16)
+    rows_kpe = (torch.randn(T * K, 64, generator=g) * 0.7).to(torch.bfloat16)
+    qn = torch.randn(T, H, 512, generator=g).to(torch.bfloat16)
+    qp = torch.randn(T, H, 64, generator=g).to(torch.bfloat16)
+    ckv = torch.empty(num_pages, ps, 512, dtype=torch.bfloat16, device=DEV)
+    kpe = torch.empty(num_pages, ps, 64, dtype=torch.bfloat16, device=DEV)
+    ckv.view(-1, 512)[pick.to(DEV)] = rows_ckv.to(DEV)
+    kpe.view(-1, 64)[pick.to(DEV)] = rows_kpe.to(DEV)
+    out, lse = kernel(qn.to(DEV), qp.to(DEV), ckv, kpe, idx.to(DEV), 0.06)
+    torch.cuda.synchronize()
+    del ckv, kpe
+    local = torch.full((slots,), -1, dtype=torch.int64)
+    local[pick] = torch.arange(T * K)
+    idx_c = torch.where(idx >= 0, local[idx.clamp(min=0).long()], torch.full_like(idx, -1).long())
+    ref = oracle.attention(_bits(qn), _bits(qp), _bits(rows_ckv), _bits(rows_kpe),
+                           idx_c.to(torch.int32).numpy(), 0.06, NTHREADS)
+    _assert_parity(out.cpu(), lse.cpu(), *ref, f"{num_pages} pages of 64")
+
+
 def test_strided_inputs_and_dps_output():
     d = workloads.cfg2(T=5, seed=11)
     g = workloads.to_device(d, DEV)
