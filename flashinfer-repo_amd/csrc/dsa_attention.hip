@@ -415,7 +415,7 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
     return a;
   };
   auto fire_tile = [&](int j, const TileSrc &a) {
-    char *st = lds + (j % kStages) * kStageBytes;
+    char *st = lds + (j & (kStages - 1)) * kStageBytes;
     char *kdst = st + kCkvStageBytes + grp * kKpeGroupPitch;
     if constexpr (NARROW) {
 #pragma unroll
@@ -684,16 +684,20 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
   // longer, which is what the fourth stage is for; two tiles remain in
   // flight.
   bf16x8 p_hi = {}, p_lo = {};
+  int next_refill = 16;  // the next tile index whose issue triggers a slot-id refill
   for (int i = 0; i < n_tiles; ++i) {
     wait_tile(i);
     if constexpr (kShared) __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's words of tile i-1 written
     __builtin_amdgcn_s_barrier();  // every wave's share of tile i landed (and tile i-1's words)
     if constexpr (kShared)
       if (i > 0) consume_words(__builtin_amdgcn_readlane(tile_masks, i - 1), p_hi, p_lo);
-    const char *st_ckv = lds + (i % kStages) * kStageBytes;
+    // stage offsets: tile i, and tile i-1 (whose stage receives tile i+3)
+    const int st_cur = (i & (kStages - 1)) * kStageBytes;
+    const int st_prev = ((i + kStages - 1) & (kStages - 1)) * kStageBytes;
+    const char *st_ckv = lds + st_cur;
     f32x4 sacc[2];
     scores(st_ckv, sacc);
-    if (i > 0) pv(lds + ((i - 1) % kStages) * kStageBytes, p_hi, p_lo);
+    if (i > 0) pv(lds + st_prev, p_hi, p_lo);
     if (FS >= 2) xput(sacc[0]);
     // (The one-slice layouts compute the addresses after the barrier: their
     // waves have no registers to hold them across it.)
@@ -715,11 +719,14 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
     if constexpr (FS >= 2) {
       static_assert(W == 8, "a half refill is 512 ids, one per lane of 8 waves");
       const int J = i + kStages - 1;
-      if (J >= 16 && J % 16 == 0 && J + 16 < n_tiles) {
-        const int key = (J + 16) * kKeysPerTile + wave * 64 + lane;  // W == 8: 512 keys
-        const int32_t *src = key < n_keys ? p.idx + (int64_t)t * p.idx_st + k_begin + key
-                                          : g_minus_one + lane;
-        lds_dma4(src, slots + ((J + 16) % L::kRingTiles) * kKeysPerTile + wave * 64);
+      if (J == next_refill) {  // J = 16, 32, ... (kept in a scalar, not tested per tile)
+        next_refill += 16;
+        if (J + 16 < n_tiles) {
+          const int key = (J + 16) * kKeysPerTile + wave * 64 + lane;  // W == 8: 512 keys
+          const int32_t *src = key < n_keys ? p.idx + (int64_t)t * p.idx_st + k_begin + key
+                                            : g_minus_one + lane;
+          lds_dma4(src, slots + ((J + 16) % L::kRingTiles) * kKeysPerTile + wave * 64);
+        }
       }
     }
     if constexpr (kShared) {
@@ -735,7 +742,7 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
       __builtin_amdgcn_s_barrier();  // the last tile's words visible
       consume_words(__builtin_amdgcn_readlane(tile_masks, n_tiles - 1), p_hi, p_lo);
     }
-    pv(lds + ((n_tiles - 1) % kStages) * kStageBytes, p_hi, p_lo);
+    pv(lds + ((n_tiles - 1) & (kStages - 1)) * kStageBytes, p_hi, p_lo);
   }
 
   // ---- epilogue: lanes of a head hold partial sums over disjoint keys (and,
