@@ -11,30 +11,30 @@
 // over the valid slots s_j of sparse_indices[t] (-1 = padding).
 //
 // Work decomposition.  One workgroup = one (token, top-k chunk, block of
-// head groups).  Its waves share a 4-stage LDS ring of 32-key tiles: every
-// tile is gathered with global_load_lds_dwordx4 (16 B per lane straight into
-// LDS, no VGPR staging; one 1 KB ckv row per instruction, 8 kpe rows per
-// instruction), three tiles in flight while the fourth is consumed.  The
-// gather is latency-bound, so the ring depth (bytes in flight per CU) sets
-// the bandwidth; it uses the whole 160 KB of LDS.  The chunk's slot ids are
-// staged in LDS once (4 bytes per key, so no index load sits in front of a
-// gather; the page division is a multiply by a host-computed reciprocal) and
-// the valid-key mask of every tile is kept in one VGPR (lane i: tile i).
-// Padding keys gather a zero row, which keeps the number of loads per wave
-// and tile fixed and makes the vmcnt-based stage waits exact.  Dense caches
+// head groups).  Its waves share a 4-stage LDS ring of 32-key tiles (the
+// whole 160 KB of LDS): every tile is gathered by LDS DMA (16 B per lane
+// straight into LDS, no VGPR staging; one 1 KB ckv row per instruction, 8 kpe
+// rows per instruction), two tiles in flight while two are in use.  The
+// chunk's slot ids are staged in LDS (4 bytes per key, so no index load sits
+// in front of a gather) and the valid-key mask of every tile is kept in one
+// VGPR (lane i: tile i).  Padding keys gather a zero row, which keeps the
+// number of loads per wave and tile fixed and makes the vmcnt-based stage
+// waits exact.  Dense caches
 // below 2 GB (every BASELINE shape) are gathered with buffer_load ... lds at
 // 32-bit offsets slot * row stride (one 24-bit multiply per key, one readlane
 // per row); a padding key's offset lies past the buffer's range, and an
 // out-of-range buffer load returns zeros, which the DMA writes as the row.
-// Other caches take 64-bit addresses with the page arithmetic and a zero row
-// in global memory.
+// Other caches take global_load_lds_dwordx4 at 64-bit addresses, the page
+// division as a multiply by a host-computed reciprocal, and a zero row in
+// global memory.
 //
 // Each wave belongs to one 16-head group and owns one slice of the 512 output
 // features.  Per tile:
 //   S^T[32 keys x 16 heads] = K[keys x 576] . Q^T       (bf16 MFMA 16x16x32)
 //     -- when FS > 1 waves share a head group, they split the 2 key blocks x
-//        18 k-steps of this product and add the partial S^T through LDS in a
-//        fixed order, so every wave of the group holds identical scores;
+//        576 features of this product into equal parts (QkSplit) and add the
+//        partial S^T through LDS in a fixed order, so every wave of the group
+//        holds identical scores;
 //   online softmax in fp32 (log2 domain), with the reference max moved only
 //   when scores overshoot it by more than kRescaleSlack;
 //   O^T[slice x 16 heads] += V^T[slice x 32 keys] . P^T  (bf16 MFMA 16x16x32,
@@ -281,7 +281,7 @@ struct Ring {
   static constexpr int kNFB = 32 / FS;            // 16-feature blocks per wave
   static constexpr int kRows = kKeysPerTile / W;  // ckv rows one wave gathers per tile
   static constexpr int kLoads = kRows + 1;        // + one kpe DMA (full or half)
-  static constexpr int kParts = FS >= 2 ? FS / 2 : 1;  // k-step ranges per key block
+  static constexpr int kParts = FS >= 2 ? FS / 2 : 1;  // QK parts per key block (QkSplit)
   static constexpr int kBlocks = FS >= 2 ? 1 : 2;      // key blocks one wave computes
   static_assert(W == 4 || W == 8, "gather split assumes 4 or 8 waves");
   static_assert(FS == 1 || FS == 2 || FS == 4 || FS == 8, "feature slices");
