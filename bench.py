@@ -312,7 +312,8 @@ def main():
     tflops = alg_flops / (ms_partial * 1e-3) / 1e12
     traffic = load_traffic(a.config)
     line = {
-        "metric": METRIC,
+        "metric": METRIC if a.config == "cfg2" else
+                  f"µs/call + HBM GB/s & MFMA %, DSA sparse attention H={H} topk={K} T={T} ({a.config})",
         "value": round(us, 3),
         "unit": "µs/call",
         "n_gpus": 1,
