@@ -30,7 +30,8 @@ def mismatches(actual, expected, atol, rtol):
     a = np.asarray(actual, dtype=np.float64)
     e = np.asarray(expected, dtype=np.float64)
     both_inf = np.isinf(a) & np.isinf(e) & (np.sign(a) == np.sign(e))
-    diff = np.abs(a - e)
+    with np.errstate(invalid="ignore"):  # inf - inf where both are -inf (empty rows' lse)
+        diff = np.abs(a - e)
     bad = (diff > atol) & (diff > rtol * np.abs(e))
     bad |= np.isnan(a) != np.isnan(e)
     bad &= ~both_inf
