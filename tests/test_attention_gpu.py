@@ -425,6 +425,20 @@ def test_in_kernel_merge_matches_merge_kernel_bitwise(H, T, splits):
         _assert_parity(out.cpu(), lse.cpu(), *_oracle(d), f"in-kernel merge splits={splits}")
 
 
+@pytest.mark.parametrize("H", [48, 64, 96, 256])
+def test_head_counts_match_oracle(H):
+    """Every kernel layout against the oracle: 3 groups of 16 heads (the
+    8-slice layout in 3 head blocks), 4 (one wave per group, 4 waves), 6 (2
+    groups x 4 slices in 3 head blocks) and 16 (one wave per group, 8 waves,
+    2 head blocks); the default split choice, with padding in one row."""
+    d = _heads(workloads.cfg2(T=3, seed=500 + H), H, seed=H)
+    d["sparse_indices"] = d["sparse_indices"][:, :700].clone()
+    d["sparse_indices"][1, 650:] = -1
+    print(f"head count H={H}", flush=True)
+    out, lse = _run(kernel, d)
+    _assert_parity(out, lse, *_oracle(d), f"H={H}")
+
+
 def test_in_kernel_merge_counters_reused_across_calls_and_shapes():
     """One counter buffer serves consecutive calls of different shapes and
     split counts; each result equals the merge-kernel path."""
