@@ -9,6 +9,8 @@ Hand-written HIP kernels behind a C ABI (``include/dsa_abi.h``,
   cache), ``k_append`` (quantise-on-append into the paged cache) and the
   pipeline (reference ``solution/triton/indexer_kernel.py``)
 * ``dsa_amd.workloads``: seeded synthetic inputs for the benchmark configs
+* ``dsa_amd.trace``: replay of recorded workloads (safetensors index files), as the
+  reference's test_splitk_correctness.py does
 """
 from .indexer_kernel import (k_append, new_k_cache, run_indexer_and_topk,  # noqa: F401
                              run_indexer_and_topk_paged, run_sparse_attention_pipeline)
