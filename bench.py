@@ -17,7 +17,10 @@ add a separate merge launch it is timed on its own through
 dsa_attn_fwd_partial.  That duration gives the roofline figure.
 
 Prints one JSON line (metric, value in us/call, roofline of the dominant
-kernel, and a CPU baseline: the CPU oracle timed on this host).
+kernel, and a CPU baseline: the CPU oracle timed on this host).  Repeated
+calls on one 151 MB cache find it in the 256 MB Infinity Cache; for cfg2 the
+line also carries ``config.cold_cache``: the same calls rotating through 3
+copies of the cache (453 MB), so the gathers come from HBM.
 """
 from __future__ import annotations
 
@@ -48,6 +51,10 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="budget of the CPU-oracle baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cold-copies", type=int, default=-1, metavar="N",
+                    help="also time calls that rotate through N copies of the KV cache, so no "
+                         "call finds its rows in the 256 MB Infinity Cache (default: 3 for cfg2, "
+                         "whose cache is 151 MB; 0 = off)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run 5 plain device copies of BYTES bytes (the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -307,6 +314,27 @@ def main():
     # eager (Python shim + ctypes + launches) for reference
     eager_ms = time_eager(lambda: kernel(*args), a.steps)
 
+    # Cold-cache variant: consecutive calls read different copies of the cache,
+    # together larger than the Infinity Cache, so the gathers come from HBM.
+    n_cold = a.cold_copies if a.cold_copies >= 0 else (3 if a.config == "cfg2" else 0)
+    cold = None
+    if n_cold > 0:
+        copies = [(g["ckv_cache"].clone(), g["kpe_cache"].clone()) for _ in range(n_cold)]
+        state = {"i": 0}
+
+        def cold_call():
+            c, k = copies[state["i"] % n_cold]
+            state["i"] += 1
+            kernel(g["q_nope"], g["q_pe"], c, k, g["sparse_indices"], d["sm_scale"])
+
+        per = n_cold * max(1, per_graph // n_cold)
+        ms_cold, _ = time_graph(graph_of(cold_call, per), per, a.steps, a.warmup)
+        cold = {"copies": n_cold,
+                "cache_bytes_per_copy": (g["ckv_cache"].numel() + g["kpe_cache"].numel()) * 2,
+                "us_per_call": round(ms_cold * 1e3, 3),
+                "gathered_GBps": round(alg_bytes / (ms_cold * 1e-3) / 1e9, 1)}
+        del copies
+
     us = ms_per_step * 1e3
     gbs = alg_bytes / (ms_partial * 1e-3) / 1e9          # dominant kernel
     tflops = alg_flops / (ms_partial * 1e-3) / 1e12
@@ -331,6 +359,7 @@ def main():
                    "tokens": T, "heads": H, "topk": K, "splits": splits,
                    "timing": f"HIP graphs of {per_graph} back-to-back kernel() calls, replayed",
                    "eager_us_per_call": round(eager_ms * 1e3, 3),
+                   "cold_cache": cold,
                    "launches_per_call": 1 if one_launch else 2,
                    "dominant_kernel_us": round(ms_partial * 1e3, 3),
                    "merge_and_gaps_us": round((ms_per_step - ms_partial) * 1e3, 3)},
