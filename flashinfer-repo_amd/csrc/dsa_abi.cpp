@@ -370,6 +370,18 @@ int dsa_indexer_topk(const dsa_indexer_args *a, void *stream) {
     return fail(DSA_EINVAL, "%s: misaligned pointer (e4m3 rows need 16 bytes)", fn);
   if (a->block_table && (a->page_size <= 0 || a->block_table_stride < 0))
     return fail(DSA_EINVAL, "%s: block_table needs page_size > 0 and a stride >= 0", fn);
+  if (a->block_table && a->block_table_width < ceil_div(a->num_positions, a->page_size))
+    return fail(DSA_EINVAL, "%s: block_table rows hold %lld pages, %lld positions of page size "
+                "%lld need %lld", fn, (long long)a->block_table_width,
+                (long long)a->num_positions, (long long)a->page_size,
+                (long long)ceil_div(a->num_positions, a->page_size));
+  if (a->block_table && a->block_table_stride > 0 &&
+      a->block_table_stride < a->block_table_width)
+    return fail(DSA_EINVAL, "%s: block_table stride %lld is below its width %lld", fn,
+                (long long)a->block_table_stride, (long long)a->block_table_width);
+  if (paged && (a->k_num_pages <= 0 || a->k_num_pages > 0x7fffffffLL))
+    return fail(DSA_EINVAL, "%s: k_cache needs k_num_pages >= 1 (got %lld)", fn,
+                (long long)a->k_num_pages);
   const dsa::IndexerWorkspace lay = dsa::indexer_workspace_layout(
       a->num_tokens, a->num_heads, a->num_positions, a->scores_out == nullptr);
   if (!a->workspace || a->workspace_bytes < lay.total || !aligned(a->workspace, 256))
@@ -400,6 +412,7 @@ int dsa_indexer_topk(const dsa_indexer_args *a, void *stream) {
     p.k_cache = a->k_cache;
     p.k_pages = a->k_pages;
     p.k_page_size = (int32_t)a->k_page_size;
+    p.k_num_pages = (int32_t)a->k_num_pages;
   }
   p.scores = a->scores_out ? a->scores_out : reinterpret_cast<float *>(ws + lay.scores);
   const hipError_t e = dsa::launch_indexer(p, static_cast<hipStream_t>(stream));

@@ -160,10 +160,14 @@ __global__ __launch_bounds__(kPrepThreads) void dsa_idx_prep_kernel(IndexerParam
     if (s < p.S) {
       if (p.k_cache != nullptr) {  // paged: codes and scale through the page map
         const int pg = p.k_pages[s / p.k_page_size], off = s % p.k_page_size;
-        const uint8_t *page = p.k_cache + (int64_t)pg * p.k_page_size * kKTokenBytes;
-        raw[0] = *(const uint4 *)(page + off * kIdxDim + g * 16);
-        raw[1] = *(const uint4 *)(page + off * kIdxDim + 64 + g * 16);
-        if (g == 0) p.k_cs[s] = *(const float *)(page + p.k_page_size * kIdxDim + off * 4) * 0x1p-18f;
+        if ((uint32_t)pg < (uint32_t)p.k_num_pages) {
+          const uint8_t *page = p.k_cache + (int64_t)pg * p.k_page_size * kKTokenBytes;
+          raw[0] = *(const uint4 *)(page + off * kIdxDim + g * 16);
+          raw[1] = *(const uint4 *)(page + off * kIdxDim + 64 + g * 16);
+          if (g == 0) p.k_cs[s] = *(const float *)(page + p.k_page_size * kIdxDim + off * 4) * 0x1p-18f;
+        } else if (g == 0) {  // unmapped page: a zero row of scale 0
+          p.k_cs[s] = 0.0f;
+        }
       } else {
         const uint8_t *row = p.k + (int64_t)s * kIdxDim;
         raw[0] = *(const uint4 *)(row + g * 16);
@@ -813,6 +817,14 @@ struct TopkShared {
 };
 
 // Rows with at most topk candidates: every candidate, then -1.
+// Number of candidate positions of row t: s is one iff s <= causal_limit[t]
+// and s < S.  Compared before adding one, so a limit of INT32_MAX (no limit)
+// does not wrap to a negative count.
+__device__ __forceinline__ int candidates(const IndexerParams &p, int t) {
+  const int lim = p.limit[t];
+  return lim >= p.S - 1 ? p.S : max(0, lim + 1);
+}
+
 __device__ __forceinline__ bool take_all(const IndexerParams &p, int t, int32_t *out, int n) {
   if (n > p.topk) return false;
   for (int i = threadIdx.x; i < p.topk; i += kTopkThreads) {
@@ -903,7 +915,7 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_idx_topk_kernel(IndexerParam
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // known uniform: scalar masks
   const float *row = p.scores + (int64_t)t * p.S;
   int32_t *out = p.out + (int64_t)t * p.topk;
-  const int n = max(0, min(p.S, p.limit[t] + 1));  // candidates 0..n-1
+  const int n = candidates(p, t);  // candidates 0..n-1
   if (take_all(p, t, out, n)) return;               // n > topk >= 1 below
 
   // Key e of this thread is position e*1024 + tid (coalesced), so the 64
@@ -1062,7 +1074,7 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_idx_topk_stream_kernel(Index
   const int t = blockIdx.x;
   const float *row = p.scores + (int64_t)t * p.S;
   int32_t *out = p.out + (int64_t)t * p.topk;
-  const int n = max(0, min(p.S, p.limit[t] + 1));
+  const int n = candidates(p, t);
   if (take_all(p, t, out, n)) return;
 
   uint32_t prefix = 0, mask = 0;

@@ -99,6 +99,7 @@ struct IndexerParams {
   const uint8_t *k_cache;
   const int32_t *k_pages;
   int32_t k_page_size;
+  int32_t k_num_pages;    // page ids outside [0, k_num_pages) read as zero rows
   float *k_cs;            // [S] workspace: c_s = fl32(k_scale * 2^-18), written by the prep kernel
   const float *w;         // [T][Hi]
   const int32_t *limit;   // [T]

@@ -16,7 +16,7 @@ DSA_EINVAL = 1
 DSA_EUNSUPPORTED = 2
 DSA_ELAUNCH = 3
 DSA_EWORKSPACE = 4
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 EXPORTED_SYMBOLS = (
     "dsa_attn_fwd",
@@ -81,6 +81,7 @@ class IndexerArgs(ctypes.Structure):
         ("out", _vp), ("scores_out", _vp),
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
         ("k_cache", _vp), ("k_pages", _vp), ("k_page_size", _i64),
+        ("block_table_width", _i64), ("k_num_pages", _i64),
     ]
 
 

@@ -42,11 +42,42 @@ def _codes(x: torch.Tensor, name: str) -> torch.Tensor:
     return x.contiguous()
 
 
-def run_indexer_and_topk(q_idx: torch.Tensor, k_idx: torch.Tensor, k_scale: torch.Tensor,
-                         weights: torch.Tensor, causal_limit: torch.Tensor, topk: int,
-                         block_table: Optional[torch.Tensor] = None, page_size: int = 64,
-                         return_scores: bool = False):
+# Names the reference's per-sequence entry points take
+# (solution/triton/indexer_kernel.py:345-363, solution/triton/kernel.py:184-211)
+# and this module's per-token ones do not.
+_REFERENCE_ONLY_ARGS = frozenset((
+    "q_index_fp8", "k_index_cache_fp8", "seq_lens", "seq_offsets", "batch_size",
+    "num_index_heads", "index_head_dim", "kv_cache_num_heads", "head_dim_with_scale",
+    "max_num_pages", "num_pages", "BLOCK_TOKENS", "BLOCK_HEADS", "device"))
+
+_LAYOUT_NOTE = (
+    "this build's {fn} takes the per-query-token layout, not the reference's "
+    "per-sequence one (solution/triton/{ref}): one indexer row per query token "
+    "(q_idx [T, heads, 128] e4m3fn), k_idx [S, 128] e4m3fn codes with a separate "
+    "float32 k_scale [S] (or a paged K cache, see run_indexer_and_topk_paged) instead "
+    "of the flat cache of 129-element records, and causal_limit [T] int32 (position s "
+    "is a candidate iff s <= causal_limit[t]) instead of seq_lens/seq_offsets/"
+    "batch_size.  A sequence b of the reference maps to one row with "
+    "causal_limit = seq_lens[b] - 1 and block_table[b] as its block table; the "
+    "result holds physical slots (or positions), not seq_offsets-based token ids.")
+
+
+def _reject_reference_layout(fn: str, ref: str, nargs: int, max_args: int, kwargs) -> None:
+    extra = sorted(set(kwargs) & _REFERENCE_ONLY_ARGS)
+    if nargs > max_args or extra:
+        what = (f"got {nargs} positional arguments" if nargs > max_args
+                else f"got reference-only argument(s) {', '.join(extra)}")
+        raise TypeError(f"{fn}(): {what}; " + _LAYOUT_NOTE.format(fn=fn, ref=ref))
+    unknown = sorted(set(kwargs) - _REFERENCE_ONLY_ARGS)
+    if unknown:
+        raise TypeError(f"{fn}() got unexpected keyword argument(s) {', '.join(unknown)}")
+
+
+def run_indexer_and_topk(*args, **kwargs):
     """Top-``topk`` positions (or slots) per query token.
+
+    ``run_indexer_and_topk(q_idx, k_idx, k_scale, weights, causal_limit, topk,
+    block_table=None, page_size=64, return_scores=False)``.
 
     ``score[t,s] = sum_h weights[t,h] * relu(q_idx[t,h] . k_idx[s] * k_scale[s])``
     for ``s <= causal_limit[t]`` (exact rounding order: see ``include/dsa_abi.h``).
@@ -55,7 +86,31 @@ def run_indexer_and_topk(q_idx: torch.Tensor, k_idx: torch.Tensor, k_scale: torc
     or ``[pages]`` shared by all tokens) the entries are physical slots
     ``block_table[page] * page_size + offset``.  With ``return_scores`` the
     fp32 ``[T, S]`` scores (masked entries -inf) are returned too.
+
+    Calls with the reference's per-sequence argument list
+    (``indexer_kernel.py:345-363``) raise ``TypeError`` naming the layout
+    difference.
     """
+    names = ("q_idx", "k_idx", "k_scale", "weights", "causal_limit", "topk", "block_table",
+             "page_size", "return_scores")
+    mine = {k: kwargs.pop(k) for k in names if k in kwargs}
+    _reject_reference_layout("run_indexer_and_topk", "indexer_kernel.py:345-363", len(args),
+                             len(names), kwargs)
+    bound = dict(zip(names, args))
+    for k, v in mine.items():
+        if k in bound:
+            raise TypeError(f"run_indexer_and_topk() got multiple values for argument {k!r}")
+        bound[k] = v
+    missing = [k for k in names[:6] if k not in bound]
+    if missing:
+        raise TypeError(f"run_indexer_and_topk() missing required argument(s) {', '.join(missing)}")
+    return _run_indexer_and_topk(**bound)
+
+
+def _run_indexer_and_topk(q_idx: torch.Tensor, k_idx: torch.Tensor, k_scale: torch.Tensor,
+                          weights: torch.Tensor, causal_limit: torch.Tensor, topk: int,
+                          block_table: Optional[torch.Tensor] = None, page_size: int = 64,
+                          return_scores: bool = False):
     k = _codes(k_idx, "k_idx")
     _check(k.dim() == 2 and k.shape[1] == INDEX_HEAD_DIM,
            f"k_idx must be [S, {INDEX_HEAD_DIM}], got {tuple(k.shape)}")
@@ -114,6 +169,10 @@ def _indexer(q_idx, S, weights, causal_limit, topk, block_table, page_size, retu
         else:
             _check(bt.dim() == 2 and bt.shape[0] == T, f"block_table must be [{T}, pages] or [pages]")
             bt_stride = bt.stride(0)
+        need = -(-S // int(page_size))
+        _check(bt.shape[-1] >= need,
+               f"block_table rows hold {bt.shape[-1]} pages; {S} positions of page size "
+               f"{int(page_size)} need {need}")
 
     lib = _lib.load()
     out = torch.empty((T, int(topk)), dtype=torch.int32, device=dev)
@@ -126,10 +185,12 @@ def _indexer(q_idx, S, weights, causal_limit, topk, block_table, page_size, retu
         a.k_idx, a.k_scale = flat[0].data_ptr(), flat[1].data_ptr()
     else:
         a.k_cache, a.k_pages, a.k_page_size = paged[0].data_ptr(), paged[1].data_ptr(), paged[2]
+        a.k_num_pages = paged[0].shape[0]
     a.causal_limit = lim.data_ptr()
     a.num_tokens, a.num_heads, a.head_dim, a.num_positions, a.topk = T, Hi, INDEX_HEAD_DIM, S, int(topk)
     a.block_table = bt.data_ptr() if bt is not None else None
     a.block_table_stride, a.page_size = bt_stride, int(page_size)
+    a.block_table_width = bt.shape[-1] if bt is not None else 0
     a.out = out.data_ptr() if topk else None
     a.scores_out = scores.data_ptr() if scores is not None else None
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
@@ -180,18 +241,44 @@ def k_append(k: torch.Tensor, slots: torch.Tensor, k_cache: torch.Tensor) -> tor
     return k_cache
 
 
-def run_sparse_attention_pipeline(q_idx, k_idx, k_scale, weights, causal_limit, block_table,
-                                  q_nope, q_pe, ckv_cache, kpe_cache, sm_scale, topk: int = 2048,
-                                  page_size: Optional[int] = None,
-                                  k_cache: Optional[torch.Tensor] = None,
-                                  k_pages: Optional[torch.Tensor] = None,
-                                  num_positions: Optional[int] = None):
+_PIPELINE_ARGS = ("q_idx", "k_idx", "k_scale", "weights", "causal_limit", "block_table",
+                  "q_nope", "q_pe", "ckv_cache", "kpe_cache", "sm_scale", "topk", "page_size",
+                  "k_cache", "k_pages", "num_positions")
+
+
+def run_sparse_attention_pipeline(*args, **kwargs):
     """Indexer -> top-k slots -> sparse attention, on one stream, no host sync
-    (reference ``kernel.py:184-332``).  ``page_size`` defaults to the cache's.
+    (reference ``kernel.py:184-332``).
+
+    ``run_sparse_attention_pipeline(q_idx, k_idx, k_scale, weights,
+    causal_limit, block_table, q_nope, q_pe, ckv_cache, kpe_cache, sm_scale,
+    topk=2048, page_size=None, k_cache=None, k_pages=None,
+    num_positions=None)``.  ``page_size`` defaults to the cache's.
     With ``k_cache`` (a paged fp8 K cache, see :func:`k_append`; ``k_idx`` and
     ``k_scale`` then None) the indexer reads ``num_positions`` positions
     through ``k_pages``, by default the sequence's 1-D ``block_table``.
-    Returns ``(output [T,H,512] bf16, lse [T,H] fp32 base-2, slots [T,topk])``."""
+    Returns ``(output [T,H,512] bf16, lse [T,H] fp32 base-2, slots [T,topk])``.
+    Calls with the reference's per-sequence argument list (``kernel.py:184-211``)
+    raise ``TypeError`` naming the layout difference."""
+    mine = {k: kwargs.pop(k) for k in _PIPELINE_ARGS if k in kwargs}
+    _reject_reference_layout("run_sparse_attention_pipeline", "kernel.py:184-211", len(args),
+                             len(_PIPELINE_ARGS), kwargs)
+    bound = dict(zip(_PIPELINE_ARGS, args))
+    for k, v in mine.items():
+        if k in bound:
+            raise TypeError(f"run_sparse_attention_pipeline() got multiple values for argument {k!r}")
+        bound[k] = v
+    missing = [k for k in _PIPELINE_ARGS[:11] if k not in bound]
+    if missing:
+        raise TypeError("run_sparse_attention_pipeline() missing required argument(s) "
+                        + ", ".join(missing))
+    return _pipeline(**bound)
+
+
+def _pipeline(q_idx, k_idx, k_scale, weights, causal_limit, block_table, q_nope, q_pe, ckv_cache,
+              kpe_cache, sm_scale, topk: int = 2048, page_size: Optional[int] = None,
+              k_cache: Optional[torch.Tensor] = None, k_pages: Optional[torch.Tensor] = None,
+              num_positions: Optional[int] = None):
     ps = int(page_size) if page_size is not None else (ckv_cache.shape[1] if ckv_cache.dim() == 3 else 1)
     if k_cache is not None:
         _check(k_idx is None and k_scale is None, "give k_idx/k_scale or k_cache, not both")
@@ -202,7 +289,7 @@ def run_sparse_attention_pipeline(q_idx, k_idx, k_scale, weights, causal_limit, 
         slots = run_indexer_and_topk_paged(q_idx, k_cache, pages, int(num_positions), weights,
                                            causal_limit, topk, block_table=block_table, page_size=ps)
     else:
-        slots = run_indexer_and_topk(q_idx, k_idx, k_scale, weights, causal_limit, topk,
-                                     block_table=block_table, page_size=ps)
+        slots = _run_indexer_and_topk(q_idx, k_idx, k_scale, weights, causal_limit, topk,
+                                      block_table=block_table, page_size=ps)
     out, lse = kernel(q_nope, q_pe, ckv_cache, kpe_cache, slots, sm_scale)
     return out, lse, slots

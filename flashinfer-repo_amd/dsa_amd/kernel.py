@@ -56,26 +56,47 @@ def new_split_counters(q_nope: torch.Tensor) -> torch.Tensor:
     return torch.zeros(max(nbytes // 4, 1), dtype=torch.int32, device=q_nope.device)
 
 
-# Merge counters of calls that bring none, one buffer per (device, stream):
-# calls on one stream run one after another and each leaves the counters zero.
-# A graph captured on a stream whose buffer an eager call has already made
-# large enough uses that buffer in every replay; otherwise (a buffer made
-# during capture would only be zeroed when the graph first replays) the
-# captured call merges with the separate merge kernel.
+# Merge counters of calls that bring none.  Each (device, stream) has two
+# zeroed buffers: one for eager calls and one for calls captured into HIP
+# graphs on that stream, so a graph replayed while eager calls run on its
+# capture stream does not share counters with them.  A call leaves its
+# counters zero again, so calls of one stream (and sequential replays) can
+# share a buffer.  Buffers are made (and zeroed) outside capture only: a
+# captured call that finds no large enough buffer merges with the separate
+# merge kernel instead.  A buffer that was ever handed to a call is never
+# freed -- a graph keeps its raw address -- so a buffer outgrown by a later
+# call is retired, not released.  Replaying two graphs captured on one
+# stream at the same time (on different streams) shares their buffer: pass
+# split_counters to such graphs.
 _stream_counters = {}
+_retired_counters = []
 
 
 def _default_counters(dev: torch.device, nbytes: int) -> Optional[torch.Tensor]:
-    key = (dev.index, _stream_handle(dev))
+    capturing = torch.cuda.is_current_stream_capturing()
+    handle = _stream_handle(dev)
+    key = (dev.index, handle, capturing)
     buf = _stream_counters.get(key)
     if buf is not None and buf.numel() * 4 >= nbytes:
         return buf
-    if torch.cuda.is_current_stream_capturing():
+    if capturing:
         return None
     words = max(nbytes // 4, 2 * buf.numel() if buf is not None else 0, 4096)
-    buf = torch.zeros(words, dtype=torch.int32, device=dev)
-    _stream_counters[key] = buf
-    return buf
+    for k in (key, (dev.index, handle, True)):
+        old = _stream_counters.get(k)
+        if old is not None and old.numel() >= words:
+            continue
+        if old is not None:
+            _retired_counters.append(old)
+        _stream_counters[k] = torch.zeros(words, dtype=torch.int32, device=dev)
+    return _stream_counters[key]
+
+
+def _rezero_counters(cnt: torch.Tensor) -> None:
+    """After a call that failed, its counters may not be zero: clear them
+    (outside capture; a failed captured call invalidates the capture anyway)."""
+    if not torch.cuda.is_current_stream_capturing():
+        cnt.zero_()
 
 
 def _inner_contiguous(x: torch.Tensor) -> torch.Tensor:
@@ -104,6 +125,12 @@ def _attn_args(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, num
     """Validate the reference tensor contract (``kernel.py:138-151``) and build
     the ``dsa_attn_args`` struct; returns ``(args, keep_alive, T, H, K, dev)``
     with output/lse/workspace still unset."""
+    if isinstance(sm_scale, torch.Tensor):
+        _check(sm_scale.numel() == 1, "sm_scale must be a number or a one-element tensor")
+        if sm_scale.device.type != "cpu" and torch.cuda.is_current_stream_capturing():
+            raise ValueError("sm_scale is a device tensor: reading it needs a device-to-host "
+                             "copy, which cannot happen during graph capture; pass a float")
+        sm_scale = float(sm_scale.item())
     _check(q_nope.dim() == 3 and q_pe.dim() == 3, "q_nope/q_pe must be [T, H, D]")
     T, H, dc = q_nope.shape
     _check(dc == HEAD_DIM_CKV, f"q_nope head dim must be {HEAD_DIM_CKV}, got {dc}")
@@ -124,8 +151,6 @@ def _attn_args(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, num
     ckv, pages, ps, ckv_sp, ckv_so = _cache_view(ckv_cache, HEAD_DIM_CKV, "ckv_cache")
     kpe, kpages, kps, kpe_sp, kpe_so = _cache_view(kpe_cache, HEAD_DIM_KPE, "kpe_cache")
     _check((pages, ps) == (kpages, kps), "ckv_cache and kpe_cache page layouts differ")
-    if isinstance(sm_scale, torch.Tensor):
-        sm_scale = float(sm_scale.item())
     q_nope = _inner_contiguous(q_nope)
     q_pe = _inner_contiguous(q_pe)
     idx = _inner_contiguous(sparse_indices)
@@ -188,7 +213,12 @@ def _attention(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, num
             cnt = _default_counters(dev, c_bytes)
         if cnt is not None:
             a.split_counters, a.split_counters_bytes = cnt.data_ptr(), cnt.numel() * 4
-    _lib.check("dsa_attn_fwd", lib.dsa_attn_fwd(ctypes.byref(a), _stream_handle(dev)))
+    else:
+        cnt = None
+    rc = lib.dsa_attn_fwd(ctypes.byref(a), _stream_handle(dev))
+    if rc != _lib.DSA_OK and cnt is not None:
+        _rezero_counters(cnt)
+    _lib.check("dsa_attn_fwd", rc)
     del keep
     return output, lse
 

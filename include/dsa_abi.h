@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define DSA_ABI_VERSION 3
+#define DSA_ABI_VERSION 4
 
 #define DSA_OK 0
 #define DSA_EINVAL 1      /* bad pointer, size, stride or alignment */
@@ -211,6 +211,14 @@ typedef struct dsa_indexer_args {
   const uint8_t *k_cache;
   const int32_t *k_pages;
   int64_t k_page_size;
+  /* Entries per block-table row (required with block_table: at least
+   * ceil(num_positions / page_size), the pages a selected position can
+   * fall in). */
+  int64_t block_table_width;
+  /* Pages of k_cache (required with k_cache, >= 1).  A position whose
+   * k_pages entry lies outside [0, k_num_pages) reads as a zero row with a
+   * zero scale (its score is 0); nothing outside k_cache is read. */
+  int64_t k_num_pages;
 } dsa_indexer_args;
 
 int dsa_indexer_topk(const dsa_indexer_args *args, void *stream);

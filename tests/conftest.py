@@ -36,6 +36,7 @@ def mismatches(actual, expected, atol, rtol):
     bad |= np.isnan(a) != np.isnan(e)
     bad &= ~both_inf
     bad |= np.isinf(a) != np.isinf(e)
+    bad |= np.isinf(a) & np.isinf(e) & (np.sign(a) != np.sign(e))  # +inf against -inf
     return int(bad.sum())
 
 

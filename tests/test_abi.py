@@ -37,7 +37,7 @@ def test_header_functions_are_exported():
 def test_abi_version_and_struct_layout(tmp_path):
     """The ctypes mirrors match the C structs field by field (gcc offsetof)."""
     lib = _lib.load()
-    assert lib.dsa_abi_version() == _lib.ABI_VERSION == 3
+    assert lib.dsa_abi_version() == _lib.ABI_VERSION == 4
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "dsa_abi.h"', 'int main(void){']
     for cname, cls in (("dsa_attn_args", _lib.AttnArgs), ("dsa_indexer_args", _lib.IndexerArgs),
                         ("dsa_k_append_args", _lib.KAppendArgs)):
@@ -198,6 +198,12 @@ def _idx_args(**kw):
      _lib.DSA_EINVAL, "multiple of 4"),
     (dict(k_idx=None, k_scale=None, k_cache=0x9008, k_pages=0xa000, k_page_size=64),
      _lib.DSA_EINVAL, "misaligned"),
+    # every page a selected position can fall in must have a block-table entry
+    (dict(block_table=0x7000, block_table_width=511), _lib.DSA_EINVAL, "block_table rows"),
+    (dict(block_table=0x7000, block_table_width=512, block_table_stride=256),
+     _lib.DSA_EINVAL, "below its width"),
+    (dict(k_idx=None, k_scale=None, k_cache=0x9000, k_pages=0xa000, k_page_size=64),
+     _lib.DSA_EINVAL, "k_num_pages"),
 ])
 def test_indexer_host_validation(kw, code, needle):
     lib = _lib.load()
@@ -246,3 +252,46 @@ def test_k_append_host_validation(kw, code, needle):
     a.k = 0x1000
     a.k_stride, a.page_size, a.k_cache = 128, 64, 0x3000
     assert lib.dsa_indexer_k_append(ctypes.byref(a), None) == 0   # nothing to do
+
+
+def test_indexer_accepts_exact_block_table_width():
+    """ceil(S / page_size) entries per row suffice (a 1-D table has stride 0)."""
+    lib = _lib.load()
+    for S, ps, width in ((32768, 64, 512), (1000, 64, 16), (1, 64, 1)):
+        a = _idx_args(num_positions=S, block_table=0x7000, page_size=ps, block_table_width=width,
+                      num_tokens=0, q_idx=None)
+        assert lib.dsa_indexer_topk(ctypes.byref(a), None) == 0
+        a = _idx_args(num_positions=S, block_table=0x7000, page_size=ps,
+                      block_table_width=width - 1, block_table_stride=0,
+                      workspace_bytes=lib.dsa_indexer_workspace_bytes(64, 64, 128, S))
+        assert lib.dsa_indexer_topk(ctypes.byref(a), None) == _lib.DSA_EINVAL
+
+
+def test_reference_argument_lists_raise_type_error_naming_the_layout():
+    """The reference's per-sequence entry points (indexer_kernel.py:345-363,
+    kernel.py:184-211) take other arguments; calling this build's functions
+    with them must say so rather than fail on a shape check."""
+    from dsa_amd.indexer_kernel import run_indexer_and_topk, run_sparse_attention_pipeline
+    ref_indexer = [None] * 14          # q, k cache, weights, seq_lens, ..., topk
+    with pytest.raises(TypeError, match="per-query-token layout"):
+        run_indexer_and_topk(*ref_indexer)
+    with pytest.raises(TypeError, match="seq_lens"):
+        run_indexer_and_topk(None, None, None, None, None, 2048, seq_lens=None)
+    with pytest.raises(TypeError, match="per-sequence"):
+        run_sparse_attention_pipeline(*([None] * 19))
+    with pytest.raises(TypeError, match="batch_size"):
+        run_indexer_and_topk(q_index_fp8=None, batch_size=4)
+    with pytest.raises(TypeError, match="unexpected keyword"):
+        run_indexer_and_topk(None, None, None, None, None, 8, bogus=1)
+    with pytest.raises(TypeError, match="missing required"):
+        run_indexer_and_topk(None, None, None)
+    with pytest.raises(TypeError, match="multiple values"):
+        run_indexer_and_topk(None, None, None, None, None, 8, topk=8)
+
+
+def test_sm_scale_tensor_must_be_one_element():
+    from dsa_amd import kernel
+    d = workloads.cfg1()
+    with pytest.raises(ValueError, match="one-element"):
+        kernel(d["q_nope"], d["q_pe"], d["ckv_cache"], d["kpe_cache"], d["sparse_indices"],
+               torch.ones(2))

@@ -483,3 +483,51 @@ def test_in_kernel_merge_graph_replays():
         ref_out, ref_lse = _merge_kernel_path(*args, 0)
         torch.cuda.synchronize()
         assert torch.equal(gout, ref_out) and torch.equal(glse, ref_lse), f"replay {i}"
+
+
+def test_captured_counters_outlive_a_larger_eager_call():
+    """A graph captured on a stream keeps the counter buffer it was given even
+    after a larger eager split call on that stream needs a bigger one: the old
+    buffer is retired, not freed, so new tensors allocated afterwards cannot
+    land on it.  Every replay equals the merge-kernel path, and the graph's
+    counters are not the ones eager calls on its stream use."""
+    import importlib
+    kmod = importlib.import_module("dsa_amd.kernel")
+    d = workloads.cfg2(T=24, seed=321)
+    g = workloads.to_device(d, DEV)
+    args = (g["q_nope"], g["q_pe"], g["ckv_cache"], g["kpe_cache"], g["sparse_indices"],
+            d["sm_scale"])
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        kernel(*args)                      # makes the stream's eager and capture counters
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        gout, glse = kernel(*args)
+    dev = torch.device(DEV)
+    cap = kmod._stream_counters[(dev.index, s.cuda_stream, True)]
+    eag = kmod._stream_counters[(dev.index, s.cuda_stream, False)]
+    assert cap.data_ptr() != eag.data_ptr()
+    # a larger eager split call on the capture stream: 600 tokens x 8 words
+    # exceed the first buffers (4096 words), so both are replaced
+    big = workloads.to_device(workloads.cfg2(T=600, seed=322), DEV)
+    print("eager T=600 split call on the capture stream", flush=True)
+    with torch.cuda.stream(s):
+        kernel_splitk(big["q_nope"], big["q_pe"], big["ckv_cache"], big["kpe_cache"],
+                      big["sparse_indices"], d["sm_scale"], SPLIT_K=2)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    assert kmod._stream_counters[(dev.index, s.cuda_stream, True)].data_ptr() != cap.data_ptr()
+    assert any(r.data_ptr() == cap.data_ptr() for r in kmod._retired_counters)
+    del big
+    filler = [torch.full((1 << 16,), -1, dtype=torch.int32, device=DEV) for _ in range(64)]
+    torch.cuda.synchronize()
+    for i in range(3):
+        graph.replay()
+        ref_out, ref_lse = _merge_kernel_path(*args, 0)
+        torch.cuda.synchronize()
+        assert torch.equal(gout, ref_out) and torch.equal(glse, ref_lse), f"replay {i}"
+        assert int((cap != 0).sum()) == 0
+    assert all(bool((f == -1).all()) for f in filler)

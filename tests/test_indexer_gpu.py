@@ -230,6 +230,21 @@ def test_long_rows_every_topk_variant(S):
     _assert_same(got_idx, got_sc, ref_idx, ref_sc, f"S={S}")
 
 
+@pytest.mark.parametrize("S", [3000, 40000])
+def test_causal_limit_extremes(S):
+    """Limits at the ends of int32 (INT32_MAX: no limit; INT32_MIN: no
+    candidate), around S and around 0, in the register top-k (S=3000) and the
+    streaming one (S=40000), against the oracle (int64 limits)."""
+    lims = [2**31 - 1, -2**31, S - 1, S, S - 2, -1, 0, 1]
+    d = workloads.indexer_inputs(T=len(lims), Hi=16, S=S, seed=7 + S)
+    d["causal_limit"] = torch.tensor(lims, dtype=torch.int32)
+    print(f"causal limit extremes S={S}", flush=True)
+    got_idx, got_sc = _gpu_indexer(d, 300)
+    ref_idx, ref_sc = _oracle(d, 300)
+    _assert_same(got_idx, got_sc, ref_idx, ref_sc, f"limit extremes S={S}")
+    assert (got_idx[0] >= 0).all() and (got_idx[1] == -1).all()
+
+
 def test_graph_replays_match_eager():
     d = workloads.indexer_inputs(T=8, Hi=64, S=5000, seed=21)
     g = workloads.to_device(d, DEV)
@@ -346,3 +361,37 @@ def test_pipeline_over_paged_k_cache_equals_flat():
     torch.cuda.synchronize()
     for a, b in zip(flat, paged):
         assert torch.equal(a, b)
+
+
+def test_paged_indexer_unmapped_pages_read_as_zero_rows():
+    """k_pages entries outside [0, pages) (a -1 or a stale id) read as zero
+    codes with scale 0 -- score 0 -- and nothing outside the cache is read:
+    the result equals the flat call with those positions zeroed."""
+    from dsa_amd import k_append, new_k_cache, run_indexer_and_topk_paged
+    g = torch.Generator().manual_seed(52)
+    T, Hi, S, ps, topk = 6, 32, 1000, 64, 200
+    d = workloads.indexer_inputs(T=T, Hi=Hi, S=S, seed=53)
+    n_pages = -(-S // ps)
+    k = torch.randn(S, 128, generator=g).to(torch.bfloat16)
+    page_of = torch.arange(n_pages, dtype=torch.int32)
+    cache = new_k_cache(n_pages, ps, DEV)
+    pos = torch.arange(S)
+    k_append(k.to(DEV), (page_of[pos // ps] * ps + pos % ps).to(torch.int32).to(DEV), cache)
+    page_of[2] = -1
+    page_of[5] = n_pages + 3
+    page_of[7] = 2**31 - 1
+    codes, scale = oracle.quantize_k(k.float().numpy())
+    for pg in (2, 5, 7):
+        codes[pg * ps:(pg + 1) * ps] = 0
+        scale[pg * ps:(pg + 1) * ps] = 0.0
+    flat = dict(d, k_idx=torch.from_numpy(codes), k_scale=torch.from_numpy(scale))
+    ref_idx, ref_sc = _gpu_indexer(flat, topk)
+    gd = workloads.to_device(d, DEV)
+    print("paged indexer with unmapped pages", flush=True)
+    out, sc = run_indexer_and_topk_paged(gd["q_idx"], cache, page_of.to(DEV), S, gd["weights"],
+                                         gd["causal_limit"], topk, return_scores=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(sc.cpu().numpy().view(np.uint32), ref_sc.view(np.uint32))
+    assert np.array_equal(out.cpu().numpy(), ref_idx)
+    ora_idx, ora_sc = _oracle(flat, topk)
+    _assert_same(ref_idx, ref_sc, ora_idx, ora_sc, "flat with zeroed pages")

@@ -363,3 +363,41 @@ def test_k_cache_pack_unpack_roundtrip():
         touched[pg, off * 128:(off + 1) * 128] = True
         touched[pg, ps * 128 + off * 4:ps * 128 + off * 4 + 4] = True
     assert np.array_equal(cache[~touched], base[~touched])
+
+
+def test_mismatch_helper_counts_signs_of_infinity_and_nans():
+    """The tolerance check of every parity test: fail iff |d| > atol and
+    |d| > rtol*|e|; infinities must match in sign, NaN only NaN."""
+    from conftest import mismatches
+    inf = np.inf
+    assert mismatches([inf, -inf], [-inf, inf], 1e-3, 1e-3) == 2
+    assert mismatches([inf, -inf], [inf, -inf], 1e-3, 1e-3) == 0
+    assert mismatches([-inf, 1.0], [0.0, -inf], 1e-3, 1e-3) == 2
+    assert mismatches([np.nan, 1.0], [1.0, np.nan], 1e-3, 1e-3) == 2
+    assert mismatches([np.nan], [np.nan], 1e-3, 1e-3) == 0
+    # both bounds must be exceeded
+    assert mismatches([1.02], [1.0], 1e-2, 1e-2) == 1
+    assert mismatches([1.005], [1.0], 1e-2, 1e-2) == 0
+    assert mismatches([100.5], [100.0], 1e-2, 1e-2) == 0     # rel 0.5 % passes
+    assert mismatches([0.015], [0.0], 1e-2, 1e-2) == 1
+
+
+def test_torch_fp32_restatement_matches_fp64_oracle():
+    """oracle.torch_ref.run_fp32 (the CPU baseline bench.py times) agrees with
+    the pinned fp64 oracle within the reference checker's tolerances, on
+    padded, empty, duplicate-slot and outlier rows and several page sizes."""
+    from conftest import LSE_ATOL, LSE_RTOL, OUT_ATOL, OUT_RTOL, mismatches
+    from oracle.torch_ref import run_fp32
+    for T, H, K, slots, ps, pad in ((4, 16, 256, 4096, 1, 0.2), (3, 32, 100, 1024, 64, 0.0),
+                                    (2, 48, 33, 128, 4, 0.5)):
+        qn, qp, ckv, kpe, idx = _rand_case(T, H, K, slots, ps, seed=500 + K, pad_frac=pad)
+        ckv.view(-1, 512)[::13] *= 8                      # outlier rows
+        idx[0] = -1                                        # an empty row
+        idx[-1, 1] = idx[-1, 0]                            # a duplicate slot counts twice
+        scale = 1 / math.sqrt(192)
+        out, lse = run_fp32(qn, qp, ckv, kpe, idx, scale)
+        ref_bits, ref_lse = _oracle(qn, qp, ckv, kpe, idx, scale)
+        want = oracle.bf16_bits_to_f32(ref_bits)
+        assert mismatches(out.float().numpy(), want, OUT_ATOL, OUT_RTOL) == 0
+        assert mismatches(lse.numpy(), ref_lse, LSE_ATOL, LSE_RTOL) == 0
+        assert torch.isneginf(lse[0]).all() and not out[0].float().abs().sum()
