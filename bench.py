@@ -1,4 +1,4 @@
-"""Benchmark of the DSA decode hot path on one MI355X.
+"""Benchmark of the DSA sparse-attention hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2]
 
@@ -11,22 +11,38 @@ the figure is the GPU time of back-to-back calls rather than Python/ctypes
 launch overhead (the eager per-call time is reported alongside).  Timing uses
 HIP events on the stream the kernels run on: W untimed warm-up steps, then K
 timed steps between synchronisations.  The dominant kernel is the gather
-attention: at H=16 a call is that one launch (the split merge runs inside
-it), so the graph time per call is its duration; for head counts whose calls
-add a separate merge launch it is timed on its own through
-dsa_attn_fwd_partial.  That duration gives the roofline figure.
+attention: where a call is that one launch (the split merge inside it, or no
+split) the graph time per call is its duration; otherwise it is timed on its
+own through dsa_attn_fwd_partial.  That duration gives the roofline figure.
 
-Prints one JSON line (metric, value in us/call, roofline of the dominant
-kernel, and a CPU baseline: the CPU oracle timed on this host).  Repeated
-calls on one 151 MB cache find it in the 256 MB Infinity Cache; for cfg2 the
-line also carries ``config.cold_cache``: the same calls rotating through 3
-copies of the cache (453 MB), so the gathers come from HBM.
+The default run prints one JSON line for config 2 (metric, value in us/call,
+roofline of the dominant kernel, the CPU baseline) and carries the other
+workloads under ``workloads``: config 1, prefill config 3 (roofline
+``mfma``), config 4 (H=128), config 5 (indexer + top-k -> attention) and
+``t1``, the shape of the reference's only published timing (T=1, 8462 pages),
+next to its RTX 6000 Ada figures.  ``--config X`` prints the line of one
+workload only (for profiler runs).
+
+Repeated calls on one 151 MB cache find it in the 256 MB Infinity Cache; the
+config 2 line also carries ``config.cold_cache``: the same calls rotating
+through 3 copies of the cache (453 MB), so the gathers come from HBM.
+
+``roofline.traffic`` is the HBM bytes per launch that rocprofv3 counters
+measured (profiles/traffic.json), used only when that record was made from
+the kernel sources of this tree (its csrc hash matches); otherwise null.
+
+The CPU baseline is the torch fp32 restatement of the reference's run()
+(oracle/torch_ref.py: whole-cache fp32 conversion, then a per-token loop) on
+the host's cores, 1 warm-up and 3 timed calls, median -- a reported
+baseline, not a target.
 """
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -38,6 +54,15 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 INT8_PEAK_TOPS = 5000.0      # dense int8 MFMA (= the fp8 dense peak)
 GRAPH_CALLS = 20
+EXTRA_STEPS = 100            # timed calls per extra workload of the default run
+ATTN_CONFIGS = ("cfg1", "cfg2", "cfg3", "cfg4", "t1")
+
+# The reference's published T=1 figures (RTX 6000 Ada, docs/PROFILING.md:47-48,
+# docs/SPLITK_OPTIMIZATION.md:140-148,159-163) -- context for the t1 workload.
+T1_REFERENCE = {"hardware": "NVIDIA RTX 6000 Ada (reference docs)",
+                "dsa_fwd_kernel_us": 92.4, "kernel_wall_us": 97.0,
+                "best_splitk_wall_us": 68.3, "best_splitk_forward_kernel_us": 4.29,
+                "sources": "docs/PROFILING.md:47-48, docs/SPLITK_OPTIMIZATION.md:140-163"}
 
 
 def parse():
@@ -45,16 +70,13 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="cfg2", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"],
-                    help="cfg1-cfg4: sparse attention; cfg5: lightning indexer + top-k "
-                         "feeding the cfg2 attention")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0,
-                    help="budget of the CPU-oracle baseline sample")
+    ap.add_argument("--config", default=None, choices=list(ATTN_CONFIGS) + ["cfg5"],
+                    help="only this workload (default: cfg2 with every other workload "
+                         "carried in the line)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cold-copies", type=int, default=-1, metavar="N",
-                    help="also time calls that rotate through N copies of the KV cache, so no "
-                         "call finds its rows in the 256 MB Infinity Cache (default: 3 for cfg2, "
-                         "whose cache is 151 MB; 0 = off)")
+                    help="also time cfg2 calls rotating through N copies of the KV cache "
+                         "(default 3: 453 MB, beyond the 256 MB Infinity Cache; 0 = off)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run 5 plain device copies of BYTES bytes (the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -71,45 +93,101 @@ def copy_calibration(nbytes: int) -> None:
     print(json.dumps({"copy_calibration_bytes": nbytes, "copies": 5}), flush=True)
 
 
+def csrc_hash() -> str:
+    """sha256 over the kernel and ABI sources (the code a traffic record measured)."""
+    h = hashlib.sha256()
+    csrc = os.path.join(ROOT, "flashinfer-repo_amd", "csrc")
+    files = sorted(os.path.join(csrc, f) for f in os.listdir(csrc)
+                   if f.endswith((".hip", ".cpp", ".h")))
+    for p in files + [os.path.join(ROOT, "include", "dsa_abi.h")]:
+        h.update(os.path.basename(p).encode())
+        with open(p, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
 def load_traffic(config: str):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3
-    --pmc summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated), or None."""
-    path = os.path.join(ROOT, "profiles", "traffic.json")
+    --pmc record (FETCH_SIZE + WRITE_SIZE, copy-calibrated), or None when no
+    record exists for this workload or it was made from other kernel sources."""
     try:
-        with open(path) as f:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
             t = json.load(f)
     except (OSError, ValueError):
         return None
     ent = t.get(config)
-    return None if ent is None else ent.get("hbm_bytes_per_launch")
+    if not ent or ent.get("csrc_sha256") != csrc_hash():
+        return None
+    return ent.get("hbm_bytes_per_launch")
 
 
-def cpu_baseline(d, budget_s: float):
-    """Times the CPU oracle (the restatement of the reference's run()) on the
-    same workload, whole calls, until the budget is spent."""
+def host_cpu():
+    """(model name, logical CPUs) of this host."""
+    model = None
+    try:
+        out = subprocess.run(["lscpu"], stdout=subprocess.PIPE, stderr=subprocess.DEVNULL,
+                             text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return model, os.cpu_count()
+
+
+def cpu_baseline(d):
+    """The torch fp32 restatement of run() (oracle/torch_ref.py) on the host:
+    1 warm-up and 3 timed whole calls, median."""
+    import torch
+
+    from oracle.torch_ref import run_fp32
+    threads = torch.get_num_threads()   # the box's CPU share (OMP_NUM_THREADS) of the host
+    args = (d["q_nope"], d["q_pe"], d["ckv_cache"], d["kpe_cache"], d["sparse_indices"],
+            d["sm_scale"])
+    run_fp32(*args)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run_fp32(*args)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    model, ncpu = host_cpu()
+    T = d["q_nope"].shape[0]
+    return {"value": round(times[1] * 1e6, 1), "unit": "µs/call", "cores": threads, "kind": "port",
+            "sample": f"whole {T}-token calls of the torch fp32 restatement of run() "
+                      f"(indexer_kernel.py:436-497: whole-cache fp32 conversion, per-token "
+                      f"loop), median of 3 after 1 warm-up: "
+                      f"{', '.join(f'{x:.3f}' for x in times)} s",
+            "host": {"lscpu_model": model, "logical_cpus": ncpu, "torch_threads": threads}}
+
+
+def cpu_indexer_baseline(d, budget_s: float = 10.0):
+    """The exact-score CPU oracle + top-k on a bounded sample of cfg5's rows
+    (whole rows over all positions), scaled to the 64-row call."""
     import numpy as np
     import torch
 
     import oracle
-
-    def bits(t):
-        return t.contiguous().view(torch.int16).numpy().view(np.uint16)
-
-    args = (bits(d["q_nope"]), bits(d["q_pe"]), bits(d["ckv_cache"]), bits(d["kpe_cache"]),
-            d["sparse_indices"].numpy(), d["sm_scale"])
-    threads = min(16, os.cpu_count() or 1)
-    oracle.attention(*args, nthreads=threads)  # warm-up (page-in, thread pool)
+    threads = torch.get_num_threads()
+    T = d["q_idx"].shape[0]
+    lim = d["causal_limit"].numpy().astype(np.int64)
+    qa, ka = d["q_idx"].numpy(), d["k_idx"].numpy()
+    sc, w = d["k_scale"].numpy(), d["weights"].numpy()
+    rows = 4
+    oracle.indexer_scores(qa[:1], ka, sc, w[:1], lim[:1], threads)  # warm-up
     n, t0 = 0, time.perf_counter()
     while True:
-        oracle.attention(*args, nthreads=threads)
+        i = (n * rows) % T
+        s = oracle.indexer_scores(qa[i:i + rows], ka, sc, w[i:i + rows], lim[i:i + rows], threads)
+        oracle.topk(s, lim[i:i + rows], int(d["topk"]))
         n += 1
         el = time.perf_counter() - t0
-        if el >= budget_s or n >= 1000:
+        if el >= budget_s or n * rows >= 2 * T:
             break
-    T = d["q_nope"].shape[0]
-    return {"value": el / n * 1e6, "unit": "µs/call", "cores": threads, "kind": "port",
-            "sample": f"{n} full calls of the {T}-token workload (fp64 CPU oracle, OpenMP "
-                      f"{threads} threads, {el:.1f} s)"}
+    return {"value": round(el / (n * rows) * T * 1e6, 1), "unit": "µs/call", "cores": threads,
+            "kind": "port",
+            "sample": f"{n * rows} of {T} token rows (exact score over all positions + top-k, "
+                      f"{threads} threads, {el:.1f} s), scaled to the {T}-row call"}
 
 
 def graph_of(fn, n):
@@ -162,51 +240,98 @@ def time_eager(fn, steps):
     return start.elapsed_time(end) / steps
 
 
-def cpu_indexer_baseline(d, budget_s: float):
-    """Times the CPU oracle's exact indexer score + top-k on a bounded sample
-    of the cfg5 rows (whole rows of all positions)."""
-    import numpy as np
-
-    import oracle
-    threads = min(16, os.cpu_count() or 1)
-    T = d["q_idx"].shape[0]
-    lim = d["causal_limit"].numpy().astype(np.int64)
-    qa, ka = d["q_idx"].numpy(), d["k_idx"].numpy()
-    sc, w = d["k_scale"].numpy(), d["weights"].numpy()
-    rows = 4
-    oracle.indexer_scores(qa[:1], ka, sc, w[:1], lim[:1], threads)  # warm-up
-    n, t0 = 0, time.perf_counter()
-    while True:
-        i = (n * rows) % T
-        s = oracle.indexer_scores(qa[i:i + rows], ka, sc, w[i:i + rows], lim[i:i + rows], threads)
-        oracle.topk(s, lim[i:i + rows], int(d["topk"]))
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or n * rows >= 10 * T:
-            break
-    per_call = el / (n * rows) * T
-    return {"value": per_call * 1e6, "unit": "µs/call", "cores": threads, "kind": "port",
-            "sample": f"{n * rows} of {T} token rows (exact score over all positions + top-k, "
-                      f"OpenMP {threads} threads, {el:.1f} s), scaled to the {T}-row call"}
-
-
-def bench_indexer(a):
-    """cfg5: the lightning indexer + top-k (block-table slots) and the whole
-    indexer -> attention pipeline."""
+def measure_attention(name, d, steps, warmup, cold_copies=0):
+    """Times kernel() on workload d; returns the fields of its line."""
     import torch
 
+    from dsa_amd import _lib, kernel, kernel_partial, num_splits, workloads
+    g = workloads.to_device(d, "cuda:0")
+    T, H, _ = d["q_nope"].shape
+    K = d["sparse_indices"].shape[1]
+    args = (g["q_nope"], g["q_pe"], g["ckv_cache"], g["kpe_cache"], g["sparse_indices"],
+            d["sm_scale"])
+    alg_bytes = workloads.attention_bytes(d["sparse_indices"])
+    alg_flops = workloads.attention_flops(d["sparse_indices"], H)
+    per_graph = min(GRAPH_CALLS, steps)
+    ms, timed = time_graph(graph_of(lambda: kernel(*args), per_graph), per_graph, steps, warmup)
+
+    # The dominant kernel: a call of one launch (one chunk per token, or the
+    # split merge inside the attention kernel) is that launch; otherwise the
+    # gather-attention launch is timed alone and the merge kernel is the rest.
+    splits = num_splits(T, H, K)
+    one_launch = splits == 1 or _lib.load().dsa_attn_counter_bytes(T, H) > 0
+    if one_launch:
+        ms_dom = ms
+        kdesc = ("dsa_attn_ring_kernel (gather attention"
+                 + (" with the split merge inside" if splits > 1 else "")
+                 + "; the only launch of a kernel() call)")
+    else:
+        ms_dom, _ = time_graph(graph_of(lambda: kernel_partial(*args, num_splits=0), per_graph),
+                               per_graph, steps, warmup)
+        kdesc = "dsa_attn_ring_kernel (per-chunk gather attention; timed alone via dsa_attn_fwd_partial)"
+    eager_ms = time_eager(lambda: kernel(*args), steps)
+
+    cold = None
+    if cold_copies > 0:
+        copies = [(g["ckv_cache"].clone(), g["kpe_cache"].clone()) for _ in range(cold_copies)]
+        state = {"i": 0}
+
+        def cold_call():
+            c, k = copies[state["i"] % cold_copies]
+            state["i"] += 1
+            kernel(g["q_nope"], g["q_pe"], c, k, g["sparse_indices"], d["sm_scale"])
+
+        per = cold_copies * max(1, per_graph // cold_copies)
+        ms_cold, _ = time_graph(graph_of(cold_call, per), per, steps, warmup)
+        cold = {"copies": cold_copies,
+                "cache_bytes_per_copy": (g["ckv_cache"].numel() + g["kpe_cache"].numel()) * 2,
+                "us_per_call": round(ms_cold * 1e3, 3),
+                "gathered_GBps": round(alg_bytes / (ms_cold * 1e-3) / 1e9, 1),
+                "frac_of_hbm_peak": round(alg_bytes / (ms_cold * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del copies
+
+    gbs = alg_bytes / (ms_dom * 1e-3) / 1e9
+    tflops = alg_flops / (ms_dom * 1e-3) / 1e12
+    hbm = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+           "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": load_traffic(name),
+           "algorithmic_bytes": alg_bytes, "kernel": kdesc}
+    mfma = {"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 5),
+            "traffic": hbm["traffic"], "algorithmic_flops": alg_flops, "kernel": kdesc}
+    # Config 3 is the MFMA-bound shape by the target's definition (its gathers
+    # hit a 40 MB causal window the caches hold); the others are priced
+    # against HBM, with the MFMA fraction beside it.
+    roofline, other = (mfma, hbm) if name == "cfg3" else (hbm, mfma)
+    cache_slots = d["ckv_cache"].numel() // 512
+    ps = d["ckv_cache"].shape[1] if d["ckv_cache"].dim() == 3 else 1
+    return {
+        "us": ms * 1e3, "ms": ms, "timed": timed,
+        "config": {"workload": f"{name}: DSA sparse attention T={T} H={H} topk={K} "
+                               f"ckv512+kpe64 bf16, {cache_slots} slots, page_size={ps}",
+                   "tokens": T, "heads": H, "topk": K, "splits": splits,
+                   "timing": f"HIP graphs of {per_graph} back-to-back kernel() calls, replayed",
+                   "eager_us_per_call": round(eager_ms * 1e3, 3),
+                   "cold_cache": cold,
+                   "launches_per_call": 1 if one_launch else 2,
+                   "dominant_kernel_us": round(ms_dom * 1e3, 3),
+                   "merge_and_gaps_us": round((ms - ms_dom) * 1e3, 3)},
+        "roofline": roofline,
+        "other_roofline": other,
+    }
+
+
+def measure_indexer(steps, warmup):
+    """cfg5: the lightning indexer + top-k (block-table slots) and the whole
+    indexer -> attention pipeline; returns (fields, workload)."""
     from dsa_amd import kernel, workloads
     from dsa_amd.indexer_kernel import run_indexer_and_topk
 
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
     d = workloads.cfg5()
-    g = workloads.to_device(d, dev)
+    g = workloads.to_device(d, "cuda:0")
     T, Hi, D = d["q_idx"].shape
     S = d["k_idx"].shape[0]
     K = int(d["topk"])
     ia = (g["q_idx"], g["k_idx"], g["k_scale"], g["weights"], g["causal_limit"])
-    slots = run_indexer_and_topk(*ia, K, block_table=g["block_table"], page_size=64)
     attn = (g["q_nope"], g["q_pe"], g["ckv_cache"], g["kpe_cache"])
 
     def indexer():
@@ -219,27 +344,15 @@ def bench_indexer(a):
         sl = run_indexer_and_topk(*ia, K, block_table=g["block_table"], page_size=64)
         kernel(*attn, sl, d["sm_scale"])
 
-    per_graph = min(GRAPH_CALLS, a.steps)
-    ms_idx, timed_steps = time_graph(graph_of(indexer, per_graph), per_graph, a.steps, a.warmup)
-    ms_score, _ = time_graph(graph_of(scores_only, per_graph), per_graph, a.steps, a.warmup)
-    ms_pipe, _ = time_graph(graph_of(pipeline, per_graph), per_graph, a.steps, a.warmup)
-    eager_ms = time_eager(pipeline, a.steps)
-
+    per_graph = min(GRAPH_CALLS, steps)
+    ms_idx, timed = time_graph(graph_of(indexer, per_graph), per_graph, steps, warmup)
+    ms_score, _ = time_graph(graph_of(scores_only, per_graph), per_graph, steps, warmup)
+    ms_pipe, _ = time_graph(graph_of(pipeline, per_graph), per_graph, steps, warmup)
+    eager_ms = time_eager(pipeline, steps)
     ops = 2 * T * Hi * S * D                          # algorithmic dot-product ops
     tops = ops / (ms_score * 1e-3) / 1e12
-    line = {
-        "metric": "µs/call, lightning indexer + top-k -> DSA attention (cfg5)",
-        "value": round(ms_pipe * 1e3, 3),
-        "unit": "µs/call",
-        "n_gpus": 1,
-        "steps": timed_steps,
-        "warmup": a.warmup,
-        "ms_per_step": round(ms_pipe, 6),
-        "higher_is_better": False,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "fp8-e4m3 scores (exact), bf16 attention",
-        "data": "synthetic (seeded; q_idx,k_idx ~N(0,1) as e4m3, scale~U(0.5,2), w~N(0,1/8))",
+    fields = {
+        "us": ms_pipe * 1e3, "ms": ms_pipe, "timed": timed,
         "config": {"workload": f"cfg5: indexer T={T} heads={Hi} dim={D} positions={S} "
                                f"top-{K} -> block-table slots -> cfg2 attention H=16",
                    "timing": f"HIP graphs of {per_graph} back-to-back calls, replayed",
@@ -250,14 +363,33 @@ def bench_indexer(a):
                    "eager_pipeline_us": round(eager_ms * 1e3, 3)},
         "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS,
                      "unit": "TFLOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4),
-                     "traffic": None, "algorithmic_ops": ops,
-                     "kernel": "dsa_idx_prep_q_kernel + dsa_idx_score_kernel (timed via "
+                     "traffic": load_traffic("cfg5"), "algorithmic_ops": ops,
+                     "kernel": "dsa_idx_prep_kernel + dsa_idx_score_kernel (timed via "
                                "dsa_indexer_topk with topk=0)"},
     }
-    del slots
-    if not a.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_indexer_baseline(d, a.cpu_seconds)
-    print(json.dumps(line), flush=True)
+    return fields, d
+
+
+def summary(f):
+    """The compact form of a workload's figures carried in the default line."""
+    out = {"us_per_call": round(f["us"], 3), "roofline": f["roofline"]}
+    if "other_roofline" in f:
+        out["other_roofline"] = {k: f["other_roofline"][k]
+                                 for k in ("bound", "achieved", "unit", "frac")}
+    out["config"] = f["config"]
+    return out
+
+
+def line_of(f, metric, steps, warmup, dtype, data):
+    return {"metric": metric, "value": round(f["us"], 3), "unit": "µs/call", "n_gpus": 1,
+            "steps": f["timed"], "warmup": warmup, "ms_per_step": round(f["ms"], 6),
+            "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+            "data": data, "config": f["config"], "roofline": f["roofline"],
+            **({"other_roofline": f["other_roofline"]} if "other_roofline" in f else {})}
+
+
+ATTN_DATA = "synthetic (seeded; q~N(0,1), cache~N(0,0.5), distinct slots per token)"
+IDX_DATA = "synthetic (seeded; q_idx,k_idx ~N(0,1) as e4m3, scale~U(0.5,2), w~N(0,1/8))"
 
 
 def main():
@@ -272,107 +404,46 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
-    if a.config == "cfg5":
-        bench_indexer(a)
-        return
-
     import torch
 
-    from dsa_amd import _lib, kernel, kernel_partial, num_splits, workloads
+    from dsa_amd import workloads
+    torch.cuda.set_device(0)
 
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    d = workloads.CONFIGS[a.config]()
-    g = workloads.to_device(d, dev)
+    if a.config == "cfg5":
+        f, d = measure_indexer(a.steps, a.warmup)
+        line = line_of(f, "µs/call, lightning indexer + top-k -> DSA attention (cfg5)", a.steps,
+                       a.warmup, "fp8-e4m3 scores (exact), bf16 attention", IDX_DATA)
+        if not a.no_cpu_baseline:
+            line["cpu_baseline"] = cpu_indexer_baseline(d)
+        print(json.dumps(line), flush=True)
+        return
+
+    name = a.config or "cfg2"
+    d = workloads.CONFIGS[name]()
+    cold = a.cold_copies if a.cold_copies >= 0 else (3 if name == "cfg2" else 0)
+    f = measure_attention(name, d, a.steps, a.warmup, cold)
     T, H, _ = d["q_nope"].shape
     K = d["sparse_indices"].shape[1]
-    args = (g["q_nope"], g["q_pe"], g["ckv_cache"], g["kpe_cache"], g["sparse_indices"],
-            d["sm_scale"])
-    alg_bytes = workloads.attention_bytes(d["sparse_indices"])
-    alg_flops = workloads.attention_flops(d["sparse_indices"], H)
-
-    per_graph = min(GRAPH_CALLS, a.steps)
-    step_graph = graph_of(lambda: kernel(*args), per_graph)
-    ms_per_step, timed_steps = time_graph(step_graph, per_graph, a.steps, a.warmup)
-
-    # The dominant kernel.  When a kernel() call is one launch (one chunk per
-    # token, or the split merge done inside the attention kernel) that launch
-    # is the whole call; otherwise the gather-attention launch is timed alone
-    # (dsa_attn_fwd_partial) and the merge kernel accounts for the rest.
-    splits = num_splits(T, H, K)
-    one_launch = splits == 1 or _lib.load().dsa_attn_counter_bytes(T, H) > 0
-    if one_launch:
-        ms_partial = ms_per_step
-        kdesc = ("dsa_attn_ring_kernel (gather attention"
-                 + (" with the split merge inside" if splits > 1 else "")
-                 + "; the only launch of a kernel() call)")
-    else:
-        part_graph = graph_of(lambda: kernel_partial(*args, num_splits=0), per_graph)
-        ms_partial, _ = time_graph(part_graph, per_graph, a.steps, a.warmup)
-        kdesc = "dsa_attn_ring_kernel (per-chunk gather attention; timed alone via dsa_attn_fwd_partial)"
-
-    # eager (Python shim + ctypes + launches) for reference
-    eager_ms = time_eager(lambda: kernel(*args), a.steps)
-
-    # Cold-cache variant: consecutive calls read different copies of the cache,
-    # together larger than the Infinity Cache, so the gathers come from HBM.
-    n_cold = a.cold_copies if a.cold_copies >= 0 else (3 if a.config == "cfg2" else 0)
-    cold = None
-    if n_cold > 0:
-        copies = [(g["ckv_cache"].clone(), g["kpe_cache"].clone()) for _ in range(n_cold)]
-        state = {"i": 0}
-
-        def cold_call():
-            c, k = copies[state["i"] % n_cold]
-            state["i"] += 1
-            kernel(g["q_nope"], g["q_pe"], c, k, g["sparse_indices"], d["sm_scale"])
-
-        per = n_cold * max(1, per_graph // n_cold)
-        ms_cold, _ = time_graph(graph_of(cold_call, per), per, a.steps, a.warmup)
-        cold = {"copies": n_cold,
-                "cache_bytes_per_copy": (g["ckv_cache"].numel() + g["kpe_cache"].numel()) * 2,
-                "us_per_call": round(ms_cold * 1e3, 3),
-                "gathered_GBps": round(alg_bytes / (ms_cold * 1e-3) / 1e9, 1)}
-        del copies
-
-    us = ms_per_step * 1e3
-    gbs = alg_bytes / (ms_partial * 1e-3) / 1e9          # dominant kernel
-    tflops = alg_flops / (ms_partial * 1e-3) / 1e12
-    traffic = load_traffic(a.config)
-    line = {
-        "metric": METRIC if a.config == "cfg2" else
-                  f"µs/call + HBM GB/s & MFMA %, DSA sparse attention H={H} topk={K} T={T} ({a.config})",
-        "value": round(us, 3),
-        "unit": "µs/call",
-        "n_gpus": 1,
-        "steps": timed_steps,
-        "warmup": a.warmup,
-        "ms_per_step": round(ms_per_step, 6),
-        "higher_is_better": False,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded; q~N(0,1), cache~N(0,0.5), distinct slots per token)",
-        "config": {"workload": f"{a.config}: DSA sparse attention T={T} H={H} topk={K} "
-                               f"ckv512+kpe64 bf16, {d['ckv_cache'].numel() // 512} slots, "
-                               f"page_size={d['ckv_cache'].shape[1]}",
-                   "tokens": T, "heads": H, "topk": K, "splits": splits,
-                   "timing": f"HIP graphs of {per_graph} back-to-back kernel() calls, replayed",
-                   "eager_us_per_call": round(eager_ms * 1e3, 3),
-                   "cold_cache": cold,
-                   "launches_per_call": 1 if one_launch else 2,
-                   "dominant_kernel_us": round(ms_partial * 1e3, 3),
-                   "merge_and_gaps_us": round((ms_per_step - ms_partial) * 1e3, 3)},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": traffic,
-                     "algorithmic_bytes": alg_bytes,
-                     "kernel": kdesc},
-        "mfma": {"achieved_tflops": round(tflops, 2), "peak_tflops": BF16_PEAK_TFLOPS,
-                 "frac": round(tflops / BF16_PEAK_TFLOPS, 5), "algorithmic_flops": alg_flops},
-    }
+    metric = METRIC if name == "cfg2" else \
+        f"µs/call + HBM GB/s & MFMA %, DSA sparse attention H={H} topk={K} T={T} ({name})"
+    line = line_of(f, metric, a.steps, a.warmup, "bf16", ATTN_DATA)
     if not a.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(d, a.cpu_seconds)
+        line["cpu_baseline"] = cpu_baseline(d)
+    del d
+    if a.config is None:
+        # every other workload, timed in this same run
+        steps = min(a.steps, EXTRA_STEPS)
+        warm = min(a.warmup, 10)
+        extra = {}
+        for other in ("cfg1", "cfg3", "cfg4", "t1"):
+            od = workloads.CONFIGS[other]()
+            extra[other] = summary(measure_attention(other, od, steps, warm))
+            del od
+            torch.cuda.empty_cache()
+        extra["t1"]["reference_published"] = T1_REFERENCE
+        fi, _ = measure_indexer(steps, warm)
+        extra["cfg5"] = summary(fi)
+        line["workloads"] = extra
     print(json.dumps(line), flush=True)
 
 
