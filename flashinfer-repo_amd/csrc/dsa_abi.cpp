@@ -238,17 +238,32 @@ int prepare_attn(const char *fn, const dsa_attn_args *a, bool partial_only, dsa:
 
 }  // namespace
 
+namespace dsa {
+
+int attn_fwd(const char *fn, const dsa_attn_args *a, void *stream) {
+  AttnParams p = {};
+  const int rc = prepare_attn(fn, a, false, &p);
+  if (rc != DSA_OK) return rc;
+  if (a->num_tokens == 0) return ok();
+  const hipError_t e = launch_attention(p, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(DSA_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
+  return ok();
+}
+
+int set_error(int code, const char *msg) { return fail(code, "%s", msg); }
+
+size_t attn_split_workspace(int64_t T, int64_t H, int64_t K, int32_t requested) {
+  int32_t s, c;
+  choose_splits(T, H, K, requested, &s, &c);
+  return attn_workspace(T, H, s);
+}
+
+}  // namespace dsa
+
 extern "C" {
 
 int dsa_attn_fwd(const dsa_attn_args *a, void *stream) {
-  dsa::AttnParams p = {};
-  const int rc = prepare_attn("dsa_attn_fwd", a, false, &p);
-  if (rc != DSA_OK) return rc;
-  if (a->num_tokens == 0) return ok();
-  const hipError_t e = dsa::launch_attention(p, static_cast<hipStream_t>(stream));
-  if (e != hipSuccess)
-    return fail(DSA_ELAUNCH, "dsa_attn_fwd: launch failed: %s", hipGetErrorString(e));
-  return ok();
+  return dsa::attn_fwd("dsa_attn_fwd", a, stream);
 }
 
 int dsa_attn_fwd_partial(const dsa_attn_args *a, void *stream) {

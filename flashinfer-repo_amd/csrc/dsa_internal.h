@@ -82,6 +82,20 @@ hipError_t launch_attention(const AttnParams &p, hipStream_t stream);
 hipError_t launch_attention_partial(const AttnParams &p, hipStream_t stream);
 hipError_t launch_attention_merge(const AttnParams &p, hipStream_t stream);
 
+}  // namespace dsa
+
+struct dsa_attn_args;
+
+namespace dsa {
+
+// dsa_attn_fwd's validation and launch, for entry points that share it (fn
+// names the entry point in error messages).
+int attn_fwd(const char *fn, const dsa_attn_args *a, void *stream);
+// Sets the thread-local error string; returns code.
+int set_error(int code, const char *msg);
+// Workspace a split call of this shape needs (0 without a split).
+size_t attn_split_workspace(int64_t T, int64_t H, int64_t K, int32_t requested);
+
 // Lightning indexer.  Workspace layout (see indexer_workspace_layout):
 //   k_pieces [ceil(S/16)][3 pieces][2 k-steps][1024 B]  MFMA B operands, lane order
 //   k_max    [ceil(S/16)]                               max |value * 2^9| per block

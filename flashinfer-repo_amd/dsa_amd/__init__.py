@@ -4,7 +4,8 @@ Hand-written HIP kernels behind a C ABI (``include/dsa_abi.h``,
 ``libdsa_amd.so``) with a host-side mirror of the reference's entry points:
 
 * ``dsa_amd.kernel``: ``kernel``, ``kernel_splitk``, ``kernel_splitk_v2``,
-  ``kernel_out`` (reference ``solution/triton/kernel.py``)
+  ``kernel_out`` (reference ``solution/triton/kernel.py``) and
+  ``kernel_noalloc`` (no device allocation: a library-owned scratch array)
 * ``dsa_amd.indexer_kernel``: ``run_indexer_and_topk`` (flat or paged fp8 K
   cache), ``k_append`` (quantise-on-append into the paged cache) and the
   pipeline (reference ``solution/triton/indexer_kernel.py``)
@@ -14,9 +15,11 @@ Hand-written HIP kernels behind a C ABI (``include/dsa_abi.h``,
 """
 from .indexer_kernel import (k_append, new_k_cache, run_indexer_and_topk,  # noqa: F401
                              run_indexer_and_topk_paged, run_sparse_attention_pipeline)
-from .kernel import (kernel, kernel_out, kernel_partial, kernel_splitk, kernel_splitk_v2,  # noqa: F401
-                     merge_partials, new_split_counters, new_workspace, num_splits)
+from .kernel import (kernel, kernel_noalloc, kernel_out, kernel_partial, kernel_splitk,  # noqa: F401
+                     kernel_splitk_v2, merge_partials, new_split_counters, new_workspace,
+                     num_splits)
 
-__all__ = ["kernel", "kernel_splitk", "kernel_splitk_v2", "kernel_out", "kernel_partial",
+__all__ = ["kernel", "kernel_splitk", "kernel_splitk_v2", "kernel_out", "kernel_noalloc",
+           "kernel_partial",
            "merge_partials", "new_split_counters", "new_workspace", "num_splits", "run_indexer_and_topk",
            "run_indexer_and_topk_paged", "k_append", "new_k_cache", "run_sparse_attention_pipeline"]

@@ -17,9 +17,11 @@ DSA_EUNSUPPORTED = 2
 DSA_ELAUNCH = 3
 DSA_EWORKSPACE = 4
 ABI_VERSION = 4
+NOALLOC_SCRATCH_BYTES = 32 << 20   # DSA_NOALLOC_SCRATCH_BYTES
 
 EXPORTED_SYMBOLS = (
     "dsa_attn_fwd",
+    "dsa_attn_fwd_noalloc",
     "dsa_attn_fwd_partial",
     "dsa_attn_merge",
     "dsa_attn_num_splits",
@@ -121,6 +123,8 @@ def load() -> ctypes.CDLL:
             raise RuntimeError(f"{LIB_PATH} does not export {name}")
     lib.dsa_attn_fwd.argtypes = [ctypes.POINTER(AttnArgs), _vp]
     lib.dsa_attn_fwd.restype = ctypes.c_int
+    lib.dsa_attn_fwd_noalloc.argtypes = [ctypes.POINTER(AttnArgs), _vp]
+    lib.dsa_attn_fwd_noalloc.restype = ctypes.c_int
     lib.dsa_attn_fwd_partial.argtypes = [ctypes.POINTER(AttnArgs), _vp]
     lib.dsa_attn_fwd_partial.restype = ctypes.c_int
     lib.dsa_attn_merge.argtypes = [ctypes.POINTER(MergeArgs), _vp]

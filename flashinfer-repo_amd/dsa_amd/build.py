@@ -14,7 +14,7 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC_DIR = os.path.join(os.path.dirname(PKG_DIR), "csrc")
 LIB_PATH = os.path.join(PKG_DIR, "libdsa_amd.so")
 
-SOURCES = ["dsa_abi.cpp", "dsa_attention.hip", "dsa_indexer.hip"]
+SOURCES = ["dsa_abi.cpp", "dsa_attention.hip", "dsa_indexer.hip", "dsa_noalloc.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

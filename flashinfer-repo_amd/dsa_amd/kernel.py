@@ -261,6 +261,34 @@ def kernel_out(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, out
     return output, lse
 
 
+def kernel_noalloc(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, output, lse,
+                   num_splits: int = 0):
+    """Destination-passing call that allocates nothing (``dsa_attn_fwd_noalloc``):
+    split partials go to the library's per-device scratch array
+    (``NOALLOC_SCRATCH_BYTES``, 32 MiB) instead of a workspace, and are merged
+    by the separate merge kernel.  Inputs must already have contiguous last
+    dimensions and 16-byte aligned rows (nothing is copied); a split workspace
+    beyond the scratch array raises ``ValueError``.  Calls that overlap on
+    one device race on the array."""
+    for name, x in (("q_nope", q_nope), ("q_pe", q_pe), ("ckv_cache", ckv_cache),
+                    ("kpe_cache", kpe_cache), ("sparse_indices", sparse_indices)):
+        _check(x.stride(-1) == 1, f"{name} must have a contiguous last dimension")
+    a, keep, T, H, K, dev = _attn_args(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices,
+                                       sm_scale, num_splits)
+    _check(tuple(output.shape) == (T, H, HEAD_DIM_CKV) and output.dtype == torch.bfloat16
+           and output.stride(-1) == 1 and output.device == dev,
+           "output must be a [T, H, 512] bfloat16 tensor with a contiguous last dim")
+    _check(tuple(lse.shape) == (T, H) and lse.dtype == torch.float32 and lse.device == dev,
+           "lse must be a [T, H] float32 tensor")
+    a.output, a.out_stride_t, a.out_stride_h = output.data_ptr(), output.stride(0), output.stride(1)
+    a.lse, a.lse_stride_t, a.lse_stride_h = lse.data_ptr(), lse.stride(0), lse.stride(1)
+    lib = _lib.load()
+    _lib.check("dsa_attn_fwd_noalloc", lib.dsa_attn_fwd_noalloc(ctypes.byref(a),
+                                                                _stream_handle(dev)))
+    del keep
+    return output, lse
+
+
 def kernel_partial(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale,
                    num_splits: int = 0):
     """Per-chunk partials without the merge (the split half of

@@ -111,6 +111,22 @@ typedef struct dsa_attn_args {
 
 int dsa_attn_fwd(const dsa_attn_args *args, void *stream);
 
+/*
+ * dsa_attn_fwd without a caller workspace: no counterpart in the reference.
+ * For callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments and results as dsa_attn_fwd, except that workspace and
+ * split_counters must be NULL: a split call keeps its fp32 partials in a
+ * device array of DSA_NOALLOC_SCRATCH_BYTES that the library owns (one per
+ * device, held until the process ends) and merges them with the separate
+ * merge kernel.  Calls whose split workspace (dsa_attn_workspace_bytes) is
+ * larger fail with DSA_EWORKSPACE.  The call allocates and frees nothing.
+ * Calls that overlap on one device share the array and race.
+ */
+#define DSA_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+
+int dsa_attn_fwd_noalloc(const dsa_attn_args *args, void *stream);
+
 /* Split count dsa_attn_fwd will use for this shape (requested 0 = auto). */
 int32_t dsa_attn_num_splits(int64_t num_tokens, int64_t num_heads, int64_t topk,
                             int32_t requested);
