@@ -10,26 +10,29 @@
 //
 // over the valid slots s_j of sparse_indices[t] (-1 = padding).
 //
-// Work decomposition.  One workgroup = one (token, top-k chunk, block of
-// head groups).  Its waves share a 4-stage LDS ring of 32-key tiles (the
-// whole 160 KB of LDS): every tile is gathered by LDS DMA (16 B per lane
-// straight into LDS, no VGPR staging; one 1 KB ckv row per instruction, 8 kpe
-// rows per instruction), two tiles in flight while two are in use.  The
-// chunk's slot ids are staged in LDS (4 bytes per key, so no index load sits
-// in front of a gather) and the valid-key mask of every tile is kept in one
-// VGPR (lane i: tile i).  Padding keys gather a zero row, which keeps the
-// number of loads per wave and tile fixed and makes the vmcnt-based stage
-// waits exact.  Dense caches
-// below 2 GB (every BASELINE shape) are gathered with buffer_load ... lds at
-// 32-bit offsets slot * row stride (one 24-bit multiply per key, one readlane
-// per row); a padding key's offset lies past the buffer's range, and an
-// out-of-range buffer load returns zeros, which the DMA writes as the row.
-// Other caches take global_load_lds_dwordx4 at 64-bit addresses, the page
-// division as a multiply by a host-computed reciprocal, and a zero row in
-// global memory.
+// Two layouts, both one workgroup per (token, top-k chunk, block of head
+// groups), both gathering the selected rows by LDS DMA (16 B per lane
+// straight into LDS, no VGPR staging) with padding keys gathering a zero row,
+// which keeps the number of loads per block fixed and makes the vmcnt-based
+// stage waits exact.  Dense caches below 2 GB (every BASELINE shape) are
+// gathered with buffer_load ... lds at 32-bit offsets slot * row stride (one
+// 24-bit multiply per key, one readlane per row); a padding key's offset lies
+// past the buffer's range, and an out-of-range buffer load returns zeros,
+// which the DMA writes as the row.  Other caches take global_load_lds_dwordx4
+// at 64-bit addresses, the page division as a multiply by a host-computed
+// reciprocal, and a zero row in global memory.
 //
-// Each wave belongs to one 16-head group and owns one slice of the 512 output
-// features.  Per tile:
+// dsa_attn_wave_kernel (an odd number of 16-head groups: H = 16 decode and
+// prefill; described at the kernel): four independent waves, each with a
+// private two-stage ring of 16-key blocks and its keys in ascending slot
+// order, merged through LDS at the end.
+//
+// dsa_attn_ring_kernel (H a multiple of 32): the waves share a 4-stage LDS
+// ring of 32-key tiles (the whole 160 KB of LDS), two tiles in flight while
+// two are in use.  The chunk's slot ids are staged in LDS (4 bytes per key,
+// so no index load sits in front of a gather) and the valid-key mask of every
+// tile is kept in one VGPR (lane i: tile i).  Each wave belongs to one
+// 16-head group and owns one slice of the 512 output features.  Per tile:
 //   S^T[32 keys x 16 heads] = K[keys x 576] . Q^T       (bf16 MFMA 16x16x32)
 //     -- when FS > 1 waves share a head group, they split the 2 key blocks x
 //        576 features of this product into equal parts (QkSplit) and add the
@@ -47,11 +50,10 @@
 // lse directly.  Otherwise each workgroup writes an unnormalised fp32 partial
 // (acc, m, l) and the partials of a token are merged with log-sum-exp
 // weights in split order (reference merge algebra: kernel.py:461-493, -inf
-// guards :475-476), so results are deterministic: in the 8-slice layout
-// inside this kernel by the wave that finishes a feature slice last (device-
-// coherent sc1 stores and loads plus a per-wave arrival counter, no L2
-// write-back), otherwise by dsa_attn_combine_kernel.  Both give the same
-// bits.
+// guards :475-476), so results are deterministic: in the wave layout inside
+// the kernel by the wave that finishes a feature slice last (device-coherent
+// sc1 stores and loads plus a per-wave arrival counter, no L2 write-back),
+// otherwise by dsa_attn_combine_kernel.  Both give the same bits.
 //
 // MFMA 16x16x32 bf16 lane layout used throughout (lane = 16*g + r):
 //   A (16 x 32): lane holds row r, k-slots 8g..8g+7
@@ -179,6 +181,58 @@ __device__ __forceinline__ void tr_read4(const char *vsrc, bf16x8 (&av)[4]) {
   av[3] = __builtin_bit_cast(bf16x8, (u32x4){a3[0], a3[1], b3[0], b3[1]});
 }
 
+// Eight transposing reads (feature blocks F0 .. F0+7, 32 bytes apart) into
+// o, left in flight: the caller's next tr_issue8_wait / tr_wait_all waits for
+// them.  No LDS access may be issued between (the waits count LDS operations).
+template <int F0>
+__device__ __forceinline__ void tr_issue8(uint32_t va, u32x2 (&o)[8]) {
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %8 offset:%9\n\t"
+      "ds_read_b64_tr_b16 %1, %8 offset:%10\n\t"
+      "ds_read_b64_tr_b16 %2, %8 offset:%11\n\t"
+      "ds_read_b64_tr_b16 %3, %8 offset:%12\n\t"
+      "ds_read_b64_tr_b16 %4, %8 offset:%13\n\t"
+      "ds_read_b64_tr_b16 %5, %8 offset:%14\n\t"
+      "ds_read_b64_tr_b16 %6, %8 offset:%15\n\t"
+      "ds_read_b64_tr_b16 %7, %8 offset:%16"
+      : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3]), "=&v"(o[4]), "=&v"(o[5]), "=&v"(o[6]),
+        "=&v"(o[7])
+      : "v"(va), "i"(F0 * 32), "i"(F0 * 32 + 32), "i"(F0 * 32 + 64), "i"(F0 * 32 + 96),
+        "i"(F0 * 32 + 128), "i"(F0 * 32 + 160), "i"(F0 * 32 + 192), "i"(F0 * 32 + 224)
+      : "memory");
+}
+
+// tr_issue8<F0> into o, then waits until the previous batch `prev` (issued
+// before it) has landed: its registers are in/out operands of the wait, so
+// their uses cannot move above it.
+template <int F0>
+__device__ __forceinline__ void tr_issue8_wait(uint32_t va, u32x2 (&o)[8], u32x2 (&prev)[8]) {
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %16 offset:%17\n\t"
+      "ds_read_b64_tr_b16 %1, %16 offset:%18\n\t"
+      "ds_read_b64_tr_b16 %2, %16 offset:%19\n\t"
+      "ds_read_b64_tr_b16 %3, %16 offset:%20\n\t"
+      "ds_read_b64_tr_b16 %4, %16 offset:%21\n\t"
+      "ds_read_b64_tr_b16 %5, %16 offset:%22\n\t"
+      "ds_read_b64_tr_b16 %6, %16 offset:%23\n\t"
+      "ds_read_b64_tr_b16 %7, %16 offset:%24\n\t"
+      "s_waitcnt lgkmcnt(8)"
+      : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3]), "=&v"(o[4]), "=&v"(o[5]), "=&v"(o[6]),
+        "=&v"(o[7]), "+v"(prev[0]), "+v"(prev[1]), "+v"(prev[2]), "+v"(prev[3]), "+v"(prev[4]),
+        "+v"(prev[5]), "+v"(prev[6]), "+v"(prev[7])
+      : "v"(va), "i"(F0 * 32), "i"(F0 * 32 + 32), "i"(F0 * 32 + 64), "i"(F0 * 32 + 96),
+        "i"(F0 * 32 + 128), "i"(F0 * 32 + 160), "i"(F0 * 32 + 192), "i"(F0 * 32 + 224)
+      : "memory");
+}
+
+__device__ __forceinline__ void tr_wait_all(u32x2 (&prev)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(prev[0]), "+v"(prev[1]), "+v"(prev[2]), "+v"(prev[3]), "+v"(prev[4]),
+                 "+v"(prev[5]), "+v"(prev[6]), "+v"(prev[7])
+               :
+               : "memory");
+}
+
 // tr_read4 for every feature block of a wave's slice, four at a time, each
 // batch followed by its MFMAs (fn(f0, av)).
 template <int NFB, int ROWB, int F0 = 0, typename Fn>
@@ -191,6 +245,12 @@ __device__ __forceinline__ void for_tr_batches(const char *vsrc, Fn &&fn) {
     for_tr_batches<NFB, ROWB, F0 + 4>(vsrc, fn);
   }
 }
+
+// Workgroup barrier for LDS data only: this wave's LDS accesses complete
+// (lgkmcnt(0)), then s_barrier, in one statement the compiler moves no memory
+// access across.  Unlike __syncthreads() it leaves vector-memory loads (and
+// LDS DMAs) in flight.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __device__ __forceinline__ uint64_t readlane64(uint64_t v, int lane) {
   const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, lane);
@@ -284,8 +344,143 @@ struct Ring {
   static constexpr int kParts = FS >= 2 ? FS / 2 : 1;  // QK parts per key block (QkSplit)
   static constexpr int kBlocks = FS >= 2 ? 1 : 2;      // key blocks one wave computes
   static_assert(W == 4 || W == 8, "gather split assumes 4 or 8 waves");
-  static_assert(FS == 1 || FS == 2 || FS == 4 || FS == 8, "feature slices");
+  static_assert(FS == 1 || FS == 2 || FS == 4, "feature slices");
 };
+
+// A chunk's partial result from one wave: NFB feature blocks starting at
+// block fs * NFB of the 16 heads of `head`'s group, with the (m, l) pair of
+// each head.  Without split counters the partial goes to the layout of
+// dsa_attn_combine_kernel ([T][S][H][512] and [T][S][H][2]; ml_writer: the
+// one wave per head group that writes the pairs).  With counters the token's
+// chunks are merged here: a wave's feature slice depends only on the same
+// slice of the other chunks, so each wave counts arrivals on its own counter
+// and exchanges its partial through a private region in lane order (NFB x
+// 1 KB of acc, then 16 (m, l) pairs), one contiguous 1 KB per store
+// instruction.  The chunks of a token run on different XCDs, whose L2s are
+// not coherent with each other: the exchange uses sc1 accesses (device
+// coherent: written through to, and read from, the memory side, as
+// device-scope atomics are) and the wave waits for its stores to complete
+// (vmcnt(0); stores count there) before it draws a ticket.  The wave that
+// draws the last ticket resets the counter for the next launch and merges the
+// slice in split order with the merge kernel's arithmetic, so both paths give
+// the same bits whichever chunk finishes last.  Regions of workgroup (t, s,
+// blockIdx.y): its W waves' acc regions tile exactly its share of part_acc
+// (16 heads x 512 fp32 per head group) and its W x 16 pairs fit in the share
+// of part_ml the host sizes (16 pairs per head).
+template <int W, int NFB>
+__device__ __forceinline__ void split_partial(const AttnParams &p, int t, int split, int head, int wave,
+                                              int lane, int fs, const f32x4 (&acc)[NFB], float m_run,
+                                              float l_run, bool ml_writer) {
+  const int g = lane >> 4, r16 = lane & 15;
+  const int S = p.num_splits;
+  const int64_t prow = ((int64_t)t * S + split) * p.H + head;
+  if (p.counters == nullptr) {
+#pragma unroll
+    for (int fb = 0; fb < NFB; ++fb) {
+      const int f0 = (fs * NFB + fb) * 16 + 4 * g;
+      *(f32x4 *)(p.part_acc + prow * kHeadDimCkv + f0) = acc[fb];
+    }
+    if (ml_writer && lane < 16) {
+      p.part_ml[prow * 2 + 0] = m_run;
+      p.part_ml[prow * 2 + 1] = l_run;
+    }
+    return;
+  }
+  static_assert(W * NFB * 256 == kHeadsPerGroup * kHeadDimCkv, "acc regions of one head group");
+  static_assert(W * 32 <= kHeadsPerGroup * 16, "(m, l) regions");
+  const int64_t wg0 = (int64_t)t * S * gridDim.y + blockIdx.y;  // chunk s: + s * gridDim.y
+  auto acc_region = [&](int s) {
+    const int64_t w = ((wg0 + (int64_t)s * gridDim.y) * W + wave) * (NFB * 256);
+    return __builtin_amdgcn_make_buffer_rsrc(p.part_acc + w, 0, NFB * 1024, kBufferFlags);
+  };
+  auto ml_region = [&](int s) {
+    const int64_t w = ((wg0 + (int64_t)s * gridDim.y) * W + wave) * 32;
+    return __builtin_amdgcn_make_buffer_rsrc(p.part_ml + w, 0, 128, kBufferFlags);
+  };
+  {
+    const auto ar = acc_region(split);
+#pragma unroll
+    for (int fb = 0; fb < NFB; ++fb)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[fb]), ar,
+                                             (fb * 64 + lane) * 16, 0, kSC1);
+    if (lane < 16)
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, make_float2(m_run, l_run)),
+                                            ml_region(split), lane * 8, 0, kSC1);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  uint32_t *cnt = p.counters + ((int64_t)t * gridDim.y + blockIdx.y) * 8 + wave;
+  uint32_t ticket = 0;
+  if (lane == 0) ticket = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  ticket = __shfl(ticket, 0);
+  if (ticket != (uint32_t)(S - 1)) return;
+  if (lane == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  auto load_ml = [&](int s) {
+    return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(ml_region(s), r16 * 8, 0, kSC1));
+  };
+  constexpr int kB = 4;    // chunks whose loads are in flight together
+  constexpr int kF = NFB;  // feature blocks per load batch: all of the wave's
+  // The max over chunks comes first (16 chunks' pairs per round trip); with
+  // at most kB chunks it is taken from the first load batch itself (one
+  // memory round trip fewer).
+  float M = -INFINITY;
+  for (int s0 = 0; S > kB && s0 < S; s0 += 16) {
+    float mv[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) mv[j] = load_ml(min(s0 + j, S - 1)).x;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) M = fmaxf(M, mv[j]);  // clamped repeats leave the max alone
+  }
+  // Feature blocks in batches of kF; the sum L is complete after the first.
+  float L = 0.f, inv = 0.f;
+#pragma unroll
+  for (int fc = 0; fc < NFB; fc += kF) {
+    f32x4 o[kF];
+#pragma unroll
+    for (int f = 0; f < kF; ++f) o[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < S; s0 += kB) {
+      float a[kB];
+      float2 ml[kB];
+      f32x4 pa[kB][kF];
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        const int s = min(s0 + j, S - 1);
+        ml[j] = load_ml(s);
+        const auto ar = acc_region(s);
+#pragma unroll
+        for (int f = 0; f < kF; ++f)
+          pa[j][f] = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(ar, ((fc + f) * 64 + lane) * 16, 0, kSC1));
+      }
+      if (S <= kB) {
+#pragma unroll
+        for (int j = 0; j < kB; ++j) M = fmaxf(M, ml[j].x);
+      }
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        a[j] = (ml[j].x == -INFINITY) ? 0.f : fast_exp2(ml[j].x - M);
+        if (fc == 0 && s0 + j < S) L += a[j] * ml[j].y;
+      }
+#pragma unroll
+      for (int j = 0; j < kB; ++j)
+        if (s0 + j < S) {
+#pragma unroll
+          for (int f = 0; f < kF; ++f) o[f] += a[j] * pa[j][f];
+        }
+    }
+    if (fc == 0) inv = (M == -INFINITY) ? 0.f : 1.f / L;
+#pragma unroll
+    for (int f = 0; f < kF; ++f) {
+      const int f0 = (fs * NFB + fc + f) * 16 + 4 * g;
+      bf16x4 ob;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) ob[k] = (__bf16)(o[f][k] * inv);
+      *(bf16x4 *)(p.out + t * p.out_st + head * p.out_sh + f0 * 2) = ob;
+    }
+  }
+  if (ml_writer && lane < 16)
+    p.lse[t * p.lse_st + head * p.lse_sh] = (M == -INFINITY) ? -INFINITY : M + __log2f(L);
+}
 
 // NARROW: the caches are dense (slot s at byte s * row stride) and below
 // 2 GB, so the gathers address them with 32-bit offsets through buffer
@@ -312,9 +507,6 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
   const int qb0 = FS >= 2 ? (fs & 1) : 0;
   const int part = FS >= 2 ? (fs >> 1) : 0;
 
-  // the 8-slice layout shares the softmax work through LDS (softmax_publish /
-  // consume_words)
-  constexpr bool kShared = W == 8 && FS == 8;
   const int k_begin = split * p.chunk;
   const int n_keys = max(0, min(p.K, k_begin + p.chunk) - k_begin);
   const int n_tiles = (n_keys + kKeysPerTile - 1) / kKeysPerTile;
@@ -452,27 +644,8 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
     }
   };
   // Partial S^T exchange: slot w holds wave w's partial of its key block.
-  // The 8-slice layout reads single components (value_logit), so it keeps
-  // them component-major (each read is 64 consecutive words, no bank
-  // conflicts); the others read whole f32x4 per lane.
-  auto xput = [&](const f32x4 &v) {
-    if constexpr (kShared) {
-      float *x = (float *)xbuf;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) x[(wave * 4 + k) * 64 + lane] = v[k];
-    } else {
-      xbuf[wave * 64 + lane] = v;
-    }
-  };
-  auto xget = [&](int slot) -> f32x4 {
-    if constexpr (kShared) {
-      const float *x = (const float *)xbuf;
-      return f32x4{x[(slot * 4 + 0) * 64 + lane], x[(slot * 4 + 1) * 64 + lane],
-                   x[(slot * 4 + 2) * 64 + lane], x[(slot * 4 + 3) * 64 + lane]};
-    } else {
-      return xbuf[slot * 64 + lane];
-    }
-  };
+  auto xput = [&](const f32x4 &v) { xbuf[wave * 64 + lane] = v; };
+  auto xget = [&](int slot) -> f32x4 { return xbuf[slot * 64 + lane]; };
   // the group's partial S^T, added in a fixed order (after the exchange)
   auto reduce = [&](f32x4 (&sacc)[2]) {
     const int base = hg * FS;
@@ -541,96 +714,6 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
     }
     l_run += psum;
   };
-  // Probability exchange of the 8-slice layout (FS == 8, one head group):
-  // value v = b*4 + k of every lane (head r16, key b*16 + kbase + 2k) is
-  // computed by wave v alone and passed on through LDS, instead of every wave
-  // reducing the partial scores and exponentiating all 512 values.  The words
-  // live in the 128-byte padding after each kpe row group of the four stages,
-  // which neither the gather nor the score reads touch: value v, lane l at
-  // padding chunk 2v + l/32, word l%32.  A word is bf16 hi << 16 | bf16 lo; hi
-  // is never negative, so its sign bit carries "this value overshoots the
-  // reference max", and since every wave reads all 512 words they all take
-  // the same (rare) rescale branch.
-  auto pword = [&](int v, int l) -> uint32_t * {
-    const int c = 2 * v + (l >> 5);
-    return (uint32_t *)(lds + (c >> 2) * kStageBytes + kCkvStageBytes + (c & 3) * kKpeGroupPitch +
-                        1024 + (l & 31) * 4);
-  };
-  // The words of tile i are published after the partial exchange of
-  // iteration i and read after the first barrier of iteration i + 1 (which
-  // also finds tile i + 1 landed), one barrier per tile for both.  This
-  // wave's value waits in pv_pending until the words show whether the tile
-  // overshot the reference max.
-  float pv_pending = 0.f;
-  auto publish = [&](float d, bool flag) {
-    const float pv = fast_exp2(d);
-    const __bf16 hi = (__bf16)pv;
-    const __bf16 lo = (__bf16)(pv - (float)hi);
-    const uint32_t w = ((uint32_t)__builtin_bit_cast(uint16_t, hi) | (flag ? 0x8000u : 0u)) << 16 |
-                       (uint32_t)__builtin_bit_cast(uint16_t, lo);
-    *pword(wave, lane) = w;
-    pv_pending = pv;
-  };
-  // this lane's score of value v = wave (head r16, key b*16 + kbase + 2k):
-  // the partials added in the order reduce() uses; -inf when masked
-  auto value_logit = [&](uint32_t vmask) -> float {
-    const int b = wave >> 2, k = wave & 3;
-    const float *x = (const float *)xbuf;
-    float sc = x[(b * 4 + k) * 64 + lane];
-#pragma unroll
-    for (int pp = 1; pp < R::kParts; ++pp) sc += x[((b + 2 * pp) * 4 + k) * 64 + lane];
-    const bool valid = ((vmask >> (b * 16 + kbase + 2 * k)) & 1u) != 0;
-    return valid ? __builtin_fmaf(sc, p.scale_log2, -m_run) : -INFINITY;
-  };
-  auto softmax_publish = [&](uint32_t vmask) {
-    const float d = value_logit(vmask);
-    publish(d, d > kRescaleSlack);
-  };
-  // Reads the 512 words of a tile whose partial scores are still in xbuf;
-  // if any overshoots, moves the reference max to the tile's max, rescales
-  // and republishes (every wave reads the same words, so all take the branch).
-  auto consume_words = [&](uint32_t vmask, bf16x8 &p_hi, bf16x8 &p_lo) {
-    uint32_t w[8];
-    uint32_t flags = 0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      w[j] = *pword(j, lane);
-      flags |= w[j];
-    }
-    if (__ballot((flags >> 31) != 0) != 0) {
-      __builtin_amdgcn_s_barrier();  // all flags read before any word is rewritten
-      f32x4 sacc[2];
-      reduce(sacc);
-      const float c = p.scale_log2;
-      const uint32_t vm = vmask >> kbase;
-      float mx = -INFINITY;
-#pragma unroll
-      for (int bb = 0; bb < 2; ++bb)
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
-          if ((vm >> (bb * 16 + 2 * kk)) & 1u) mx = fmaxf(mx, sacc[bb][kk] * c);
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run, mx);
-      const float alpha = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - m_new);
-      m_run = m_new;
-      l_run *= alpha;
-#pragma unroll
-      for (int fb = 0; fb < R::kNFB; ++fb) acc[fb] *= alpha;
-      publish(value_logit(vmask), false);
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-      __builtin_amdgcn_s_barrier();        // republished words visible, xbuf reads done
-#pragma unroll
-      for (int j = 0; j < 8; ++j) w[j] = *pword(j, lane);
-    }
-    l_run += pv_pending;  // this wave's share; the shares are added at the end
-    // no word carries a flag here (none was set, or all were republished)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      p_hi[j] = __builtin_bit_cast(__bf16, (uint16_t)(w[j] >> 16));
-      p_lo[j] = __builtin_bit_cast(__bf16, (uint16_t)(w[j] & 0xffffu));
-    }
-  };
   // O^T += V^T . P^T over this wave's feature slice, V from the tile at st_ckv
   auto pv = [&](const char *st_ckv, const bf16x8 &p_hi, const bf16x8 &p_lo) {
     // ---- O^T += V^T . P^T over this wave's feature slice; k-slot k of lane
@@ -687,10 +770,7 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
   int next_refill = 16;  // the next tile index whose issue triggers a slot-id refill
   for (int i = 0; i < n_tiles; ++i) {
     wait_tile(i);
-    if constexpr (kShared) __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's words of tile i-1 written
-    __builtin_amdgcn_s_barrier();  // every wave's share of tile i landed (and tile i-1's words)
-    if constexpr (kShared)
-      if (i > 0) consume_words(__builtin_amdgcn_readlane(tile_masks, i - 1), p_hi, p_lo);
+    __builtin_amdgcn_s_barrier();  // every wave's share of tile i landed
     // stage offsets: tile i, and tile i-1 (whose stage receives tile i+3)
     const int st_cur = (i & (kStages - 1)) * kStageBytes;
     const int st_prev = ((i + kStages - 1) & (kStages - 1)) * kStageBytes;
@@ -729,36 +809,14 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
         }
       }
     }
-    if constexpr (kShared) {
-      softmax_publish(__builtin_amdgcn_readlane(tile_masks, i));
-    } else {
-      if (FS >= 2) reduce(sacc);
-      softmax(sacc, __builtin_amdgcn_readlane(tile_masks, i), p_hi, p_lo);
-    }
+    if (FS >= 2) reduce(sacc);
+    softmax(sacc, __builtin_amdgcn_readlane(tile_masks, i), p_hi, p_lo);
   }
-  if (n_tiles > 0) {
-    if constexpr (kShared) {
-      __builtin_amdgcn_s_waitcnt(0xC07F);
-      __builtin_amdgcn_s_barrier();  // the last tile's words visible
-      consume_words(__builtin_amdgcn_readlane(tile_masks, n_tiles - 1), p_hi, p_lo);
-    }
-    pv(lds + ((n_tiles - 1) & (kStages - 1)) * kStageBytes, p_hi, p_lo);
-  }
+  if (n_tiles > 0) pv(lds + ((n_tiles - 1) & (kStages - 1)) * kStageBytes, p_hi, p_lo);
 
-  // ---- epilogue: lanes of a head hold partial sums over disjoint keys (and,
-  // with the probability exchange, each wave over its share of the values)
+  // ---- epilogue: lanes of a head hold partial sums over disjoint keys
   l_run += __shfl_xor(l_run, 16);
   l_run += __shfl_xor(l_run, 32);
-  if constexpr (kShared) {
-    __builtin_amdgcn_s_barrier();  // every wave done with the exchange words
-    if (lane < 16) *pword(wave >> 1, (wave & 1) * 32 + lane) = __float_as_uint(l_run);
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    __builtin_amdgcn_s_barrier();
-    float l = 0.f;
-#pragma unroll
-    for (int w = 0; w < 8; ++w) l += __uint_as_float(*pword(w >> 1, (w & 1) * 32 + r16));
-    l_run = l;
-  }
   if (p.num_splits == 1 && !p.partial_only) {
     const float inv = (m_run == -INFINITY) ? 0.f : 1.f / l_run;
 #pragma unroll
@@ -775,140 +833,403 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
     return;
   }
 
-  // ---- split: write this chunk's partial
-  const int S = p.num_splits;
-  const int64_t prow = ((int64_t)t * S + split) * p.H + head;
-  // (The in-kernel merge is built for the 8-slice layout only: with fewer
-  // slices a wave owns more feature blocks, its merge takes one memory round
-  // trip per 4 of them, and the tail costs more than the merge kernel.)
-  if (FS != 8 || p.counters == nullptr) {  // dsa_attn_combine_kernel merges
+  // ---- split: this chunk's partial for dsa_attn_combine_kernel (these
+  // layouts never merge inside the kernel: a wave owns 8 or more feature
+  // blocks, so an in-kernel merge costs more memory round trips than the
+  // second launch)
+  const int64_t prow = ((int64_t)t * p.num_splits + split) * p.H + head;
 #pragma unroll
-    for (int fb = 0; fb < R::kNFB; ++fb) {
-      const int f0 = (fs * R::kNFB + fb) * 16 + 4 * g;
-      *(f32x4 *)(p.part_acc + prow * kHeadDimCkv + f0) = acc[fb];
-    }
-    if (fs == 0 && lane < 16) {
-      p.part_ml[prow * 2 + 0] = m_run;
-      p.part_ml[prow * 2 + 1] = l_run;
-    }
-    return;
+  for (int fb = 0; fb < R::kNFB; ++fb) {
+    const int f0 = (fs * R::kNFB + fb) * 16 + 4 * g;
+    *(f32x4 *)(p.part_acc + prow * kHeadDimCkv + f0) = acc[fb];
   }
+  if (fs == 0 && lane < 16) {
+    p.part_ml[prow * 2 + 0] = m_run;
+    p.part_ml[prow * 2 + 1] = l_run;
+  }
+}
 
-  if constexpr (FS == 8) {
-  // ---- in-kernel merge.  A wave's feature slice of its head group depends
-  // only on the same slice of the other chunks, so each wave counts arrivals
-  // on its own counter (no workgroup-wide flag, no barrier) and exchanges its
-  // partial through a private region in lane order (kNFB x 1 KB of acc, then
-  // 16 (m, l) pairs), one contiguous 1 KB per store instruction.  The chunks
-  // of a token run on different XCDs, whose L2s are not coherent with each
-  // other.  A device-scope release/acquire fence pair would write back /
-  // invalidate the whole L2 (buffer_wbl2 / buffer_inv), which costs more than
-  // the second launch it saves; instead the exchange uses sc1 accesses
-  // (device-coherent: written through to, and read from, the memory side, as
-  // device-scope atomics are) and the wave waits for its stores to complete
-  // (vmcnt(0); stores count there) before it draws a ticket.  The wave that
-  // draws the last ticket resets the counter for the next launch and merges
-  // the slice in split order with the merge kernel's arithmetic, so both
-  // paths give the same bits whichever chunk finishes last.
-  // Regions of workgroup (t, s, blockIdx.y): its W waves' acc regions tile
-  // exactly the workgroup's share of part_acc (kHG x 16 heads x 512 fp32),
-  // and its W x 16 (m, l) pairs fit in the share of part_ml the host sizes
-  // (kHG x 16 heads x 8 pairs).
-  static_assert(W * R::kNFB * 256 == R::kHG * kHeadsPerGroup * kHeadDimCkv, "acc regions");
-  static_assert(W * 32 <= R::kHG * kHeadsPerGroup * 16, "(m, l) regions");
-  const int64_t wg0 = (int64_t)t * S * gridDim.y + blockIdx.y;  // chunk s: + s * gridDim.y
-  auto acc_region = [&](int s) {
-    const int64_t w = ((wg0 + (int64_t)s * gridDim.y) * W + wave) * (R::kNFB * 256);
-    return __builtin_amdgcn_make_buffer_rsrc(p.part_acc + w, 0, R::kNFB * 1024, kBufferFlags);
-  };
-  auto ml_region = [&](int s) {
-    const int64_t w = ((wg0 + (int64_t)s * gridDim.y) * W + wave) * 32;
-    return __builtin_amdgcn_make_buffer_rsrc(p.part_ml + w, 0, 128, kBufferFlags);
-  };
+// ---- one head group: four independent waves --------------------------------
+//
+// Layout for head counts of an odd number of 16-head groups (H = 16 decode
+// and prefill): one workgroup per (token, top-k chunk, head group) with four
+// waves, one per SIMD.  Each wave owns a quarter of the chunk's 16-key blocks
+// (its keys taken in ascending slot order) and runs on its own: its blocks
+// are gathered by LDS DMA into a private
+// two-stage ring (block j+1 in flight while block j is computed), its scores
+// are complete (the whole 576-wide QK per wave: no partial-score exchange),
+// and its online softmax and O^T accumulator cover its own keys only.  No
+// workgroup barrier sits in the loop, so a wave waiting for a slow gather
+// does not hold the others.  After the loop the four partial results are
+// merged through LDS with log-sum-exp weights in wave order.
+//
+// Per block (16 keys):
+//   S^T[16 keys x 16 heads] = K[keys x 576] . Q^T   18 x MFMA 16x16x32 bf16
+//   O^T[512 x 16 heads]    += V^T[512 x keys] . P^T 32 x 2 x MFMA 16x16x16 bf16
+// (P in bf16 hi + lo parts).  MFMA row m of S^T is key key_of_row(m); the D
+// layout of S^T (lane 16g + c: rows 4g..4g+3 of head c) is the B-operand
+// layout of P^T for the 16x16x16 product, whose A operand (V^T, features x
+// keys 4g..4g+3) is one ds_read_b64_tr_b16 per feature block.
+//
+// Stage layout: 16 ckv rows at a 1040-byte pitch (key k at row k), then the
+// 16 kpe rows chunk-major (16-byte chunk c of key k at 256 c + 16 k), so the
+// QK operand reads (16 rows, one column) and the transposing V^T reads (rows
+// key_of_row(4g + j)) are free of bank conflicts.
+constexpr int kWaveBlock = 16;                          // keys per block
+constexpr int kWaveWaves = 4;
+constexpr int kWaveKpeOff = kWaveBlock * kCkvPitch;     // 16640
+constexpr int kWaveStage = kWaveKpeOff + kWaveBlock * 128;  // + 2048 = 18688
+constexpr int kWaveRing = 2 * kWaveStage;
+constexpr int kWaveIds = kMaxChunkWide;                 // slot ids of a chunk, staged once
+constexpr int kWaveLds = kWaveWaves * kWaveRing + kWaveIds * 4;
+static_assert(kWaveLds <= 160 * 1024, "LDS budget of one gfx950 CU");
+// the merge after the loop reuses each wave's ring: three 8 KB slices (one
+// per other wave), then 16 (m, l) pairs
+static_assert(3 * 8192 + 16 * 8 <= kWaveRing, "merge space");
+
+template <bool NARROW>
+__global__ __launch_bounds__(kWaveWaves * 64, 1) void dsa_attn_wave_kernel(AttnParams p) {
+  __shared__ __attribute__((aligned(16))) char lds[kWaveLds];
+  int32_t *slots = (int32_t *)(lds + kWaveWaves * kWaveRing);
+
+  const int t = blockIdx.x / p.num_splits;
+  const int split = blockIdx.x - t * p.num_splits;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+  const int head = blockIdx.y * kHeadsPerGroup + r16;
+  const int k_begin = split * p.chunk;
+  const int n_keys = max(0, min(p.K, k_begin + p.chunk) - k_begin);
+  const int n_blocks = (n_keys + kWaveBlock - 1) / kWaveBlock;
+  const int b0 = n_blocks * wave / kWaveWaves;  // this wave's blocks: [b0, b1)
+  const int my_blocks = n_blocks * (wave + 1) / kWaveWaves - b0;
+  char *ring = lds + wave * kWaveRing;
+
+  // Prologue: this wave's ids are loaded first, then Q^T; the ids are sorted
+  // and the first gather issued while Q is still in flight (vector loads
+  // complete in issue order, so the loop's stage waits cover Q).
+  constexpr int kPer = kWaveIds / (kWaveWaves * 64);  // ids per lane (a wave takes <= 512 keys)
+  const int32_t *isrc = p.idx + (int64_t)t * p.idx_st + k_begin + b0 * kWaveBlock;
+  const int n_mine = my_blocks * kWaveBlock;  // keys of this wave's blocks (tail padding included)
+  const int n_real = min(n_mine, n_keys - b0 * kWaveBlock);
+  int sv[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int i = k * 64 + lane;
+    sv[k] = i < n_real ? isrc[i] : -1;
+  }
+  // Q^T as the B operand of S^T = K Q^T: k-step k < 16 holds q_nope features
+  // 32k + 8g .. +7 of head `head`, k-steps 16, 17 the q_pe features.
+  bf16x8 q[18];
   {
-    const auto ar = acc_region(split);
+    const char *qn = p.q_nope + t * p.qn_st + head * p.qn_sh + g * 16;
+    const char *qp = p.q_pe + t * p.qp_st + head * p.qp_sh + g * 16;
 #pragma unroll
-    for (int fb = 0; fb < R::kNFB; ++fb)
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[fb]), ar,
-                                             (fb * 64 + lane) * 16, 0, kSC1);
-    if (lane < 16)
-      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, make_float2(m_run, l_run)),
-                                            ml_region(split), lane * 8, 0, kSC1);
+    for (int k = 0; k < 16; ++k) q[k] = *(const bf16x8 *)(qn + k * 64);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) q[16 + k] = *(const bf16x8 *)(qp + k * 64);
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  uint32_t *cnt = p.counters + ((int64_t)t * gridDim.y + blockIdx.y) * 8 + wave;
-  uint32_t ticket = 0;
-  if (lane == 0) ticket = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  ticket = __shfl(ticket, 0);
-  if (ticket != (uint32_t)(S - 1)) return;
-  if (lane == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  auto valid_id = [&](int s) { return (s >= 0 && (int64_t)s < p.num_slots) ? s : -1; };
 
-  auto load_ml = [&](int s) {
-    return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(ml_region(s), r16 * 8, 0, kSC1));
-  };
-  constexpr int kB = 4;                           // chunks whose loads are in flight together
-  constexpr int kF = R::kNFB < 4 ? R::kNFB : 4;   // feature blocks per load batch
-  // The max over chunks comes first; with at most kB chunks it is taken from
-  // the first load batch itself (one memory round trip fewer).
-  float M = -INFINITY;
-  for (int s0 = 0; S > kB && s0 < S; s0 += kB) {
-    float mv[kB];
+  // ---- order this wave's keys by slot: a stable counting sort on the top 8
+  // bits of the slot id (256 buckets, each a contiguous range of the cache),
+  // in the wave's own (not yet used) ring, so no workgroup barrier is
+  // needed: one wave's LDS accesses execute in program order.  Every wave of
+  // every workgroup then sweeps the cache upwards at the same time, which
+  // keeps address translation and cache lines shared between neighbouring
+  // gathers.  The order depends on the ids alone: results stay
+  // deterministic.  Scratch: per-vector bucket counts hist[k][256] (bytes;
+  // vector k = keys 64k .. 64k+63 of the wave), their start positions
+  // start[k][256] (u16); the sorted ids go to the wave's 512-entry slice of
+  // the id array.
+  uint8_t *hist = (uint8_t *)ring;
+  uint16_t *start = (uint16_t *)(ring + kPer * 256);
+  int32_t *my_ids = slots + wave * (kWaveIds / kWaveWaves);
+  static_assert(kPer * 256 * 3 <= kWaveRing, "sort scratch in the ring");
+  *(u32x4 *)(hist + lane * 32) = u32x4{0u, 0u, 0u, 0u};
+  *(u32x4 *)(hist + lane * 32 + 16) = u32x4{0u, 0u, 0u, 0u};
+  const uint32_t top = (uint32_t)min(p.num_slots, (int64_t)0x7fffffff);
+  const int shift = max(0, (32 - __builtin_clz(max(top, 1u))) - 8);
+  int bk[kPer], rk[kPer];
 #pragma unroll
-    for (int j = 0; j < kB; ++j) mv[j] = load_ml(min(s0 + j, S - 1)).x;
+  for (int k = 0; k < kPer; ++k) {
+    const int id = valid_id(sv[k]);
+    sv[k] = id;
+    const int b = k * 64 + lane < n_mine ? (id >= 0 ? (id >> shift) : 255) : -1;
+    bk[k] = b;
+    rk[k] = 0;
+    if (k * 64 < n_mine) {  // wave-uniform
+      uint64_t same = __ballot(b >= 0);
 #pragma unroll
-    for (int j = 0; j < kB; ++j) M = fmaxf(M, mv[j]);  // clamped repeats leave the max alone
-  }
-  // Feature blocks in batches of kF (bounded registers in the 1-slice
-  // layouts); the sum L is complete after the first batch.
-  float L = 0.f, inv = 0.f;
-#pragma unroll
-  for (int fc = 0; fc < R::kNFB; fc += kF) {
-    f32x4 o[kF];
-#pragma unroll
-    for (int f = 0; f < kF; ++f) o[f] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int s0 = 0; s0 < S; s0 += kB) {
-      float a[kB];
-      float2 ml[kB];
-      f32x4 pa[kB][kF];
-#pragma unroll
-      for (int j = 0; j < kB; ++j) {
-        const int s = min(s0 + j, S - 1);
-        ml[j] = load_ml(s);
-        const auto ar = acc_region(s);
-#pragma unroll
-        for (int f = 0; f < kF; ++f)
-          pa[j][f] = __builtin_bit_cast(
-              f32x4, __builtin_amdgcn_raw_buffer_load_b128(ar, ((fc + f) * 64 + lane) * 16, 0, kSC1));
+      for (int bit = 0; bit < 8; ++bit) {
+        const bool on = (b >> bit) & 1;
+        const uint64_t bb = __ballot(on);
+        same &= on ? bb : ~bb;
       }
-      if (S <= kB) {
-#pragma unroll
-        for (int j = 0; j < kB; ++j) M = fmaxf(M, ml[j].x);
-      }
-#pragma unroll
-      for (int j = 0; j < kB; ++j) {
-        a[j] = (ml[j].x == -INFINITY) ? 0.f : fast_exp2(ml[j].x - M);
-        if (fc == 0 && s0 + j < S) L += a[j] * ml[j].y;
-      }
-#pragma unroll
-      for (int j = 0; j < kB; ++j)
-        if (s0 + j < S) {
-#pragma unroll
-          for (int f = 0; f < kF; ++f) o[f] += a[j] * pa[j][f];
-        }
+      const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(same >> 32),
+                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)same, 0));
+      rk[k] = rank;
+      if (b >= 0 && rank == __popcll(same) - 1) hist[k * 256 + b] = (uint8_t)(rank + 1);
     }
-    if (fc == 0) inv = (M == -INFINITY) ? 0.f : 1.f / L;
+  }
+  {
+    // lane l owns buckets 4l .. 4l+3
+    uint32_t pre[kPer][4], tot[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int f = 0; f < kF; ++f) {
-      const int f0 = (fs * R::kNFB + fc + f) * 16 + 4 * g;
+    for (int k = 0; k < kPer; ++k) {
+      const uint32_t c4 = *(const uint32_t *)(hist + k * 256 + lane * 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pre[k][i] = tot[i];
+        tot[i] += (c4 >> (8 * i)) & 255u;
+      }
+    }
+    const int lsum = (int)(tot[0] + tot[1] + tot[2] + tot[3]);
+    int incl = lsum;
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xf, 0xf, false);  // row_shr:1
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xf, 0xf, false);  // row_shr:2
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xf, 0xf, false);  // row_shr:4
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xf, 0xf, false);  // row_shr:8
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    incl += __builtin_amdgcn_update_dpp(0, incl, 0x143, 0xc, 0xf, false);  // row_bcast:31
+    uint32_t base[4];
+    base[0] = (uint32_t)(incl - lsum);
+#pragma unroll
+    for (int i = 1; i < 4; ++i) base[i] = base[i - 1] + tot[i - 1];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const uint32_t lo = (base[0] + pre[k][0]) | ((base[1] + pre[k][1]) << 16);
+      const uint32_t hi = (base[2] + pre[k][2]) | ((base[3] + pre[k][3]) << 16);
+      *(u32x2 *)(start + k * 256 + lane * 4) = u32x2{lo, hi};
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kPer; ++k)
+    if (bk[k] >= 0) my_ids[start[k * 256 + bk[k]] + rk[k]] = sv[k];
+  const int id0 = my_blocks > 0 ? my_ids[r16] : -1;
+
+  const auto ckv_rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)p.ckv, 0, (int)p.ckv_extent, kBufferFlags);
+  const auto kpe_rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)p.kpe, 0, (int)p.kpe_extent, kBufferFlags);
+  constexpr uint32_t kOOB = 0x80000000u;
+
+  // Gather of a block into stage st, `id` being the slot of key r16 of the
+  // block (-1: padding): 16 ckv rows (one 1 KB DMA each, the row's offset
+  // read from its lane) and the kpe rows in two DMAs (lane l: chunk l/16 (+4)
+  // of key l%16).  Returns the block's valid-key mask (bit k: key k).  Every
+  // block issues exactly 18 loads, so the stage waits below are exact vmcnt
+  // counts.
+  auto gather = [&](int id, int st) -> uint32_t {
+    char *dst = ring + st * kWaveStage;
+    const uint32_t valid = (uint32_t)__ballot(id >= 0) & 0xffffu;
+    if constexpr (NARROW) {
+      const uint32_t co = id >= 0 ? __umul24((uint32_t)id, p.ckv_rs) : kOOB;
+      const uint32_t ko = (id >= 0 ? __umul24((uint32_t)id, p.kpe_rs) : kOOB) + g * 16;
+#pragma unroll
+      for (int m = 0; m < kWaveBlock; ++m)
+        lds_dma16_buf(ckv_rsrc, dst + m * kCkvPitch, __builtin_amdgcn_readlane(co, m) + lane * 16);
+      lds_dma16_buf(kpe_rsrc, dst + kWaveKpeOff, ko);
+      lds_dma16_buf(kpe_rsrc, dst + kWaveKpeOff + 1024, ko + 64);
+    } else {
+      uint64_t ca = (uint64_t)(const char *)g_zero_row, ka = (uint64_t)(const char *)g_zero_row;
+      if (id >= 0) {
+        const uint32_t pg = (uint32_t)(((uint64_t)(uint32_t)id * p.ps_magic) >> (31 + p.ps_shift));
+        const uint32_t of = (uint32_t)id - pg * (uint32_t)p.page_size;
+        ca = (uint64_t)(p.ckv + (int64_t)pg * p.ckv_sp + (int64_t)of * p.ckv_so);
+        ka = (uint64_t)(p.kpe + (int64_t)pg * p.kpe_sp + (int64_t)of * p.kpe_so);
+      }
+      ka += g * 16;
+#pragma unroll
+      for (int m = 0; m < kWaveBlock; ++m)
+        lds_dma16((const char *)readlane64(ca, m) + lane * 16, dst + m * kCkvPitch);
+      lds_dma16((const char *)ka, dst + kWaveKpeOff);
+      lds_dma16((const char *)ka + 64, dst + kWaveKpeOff + 1024);
+    }
+    return valid;
+  };
+  uint32_t vm_next = my_blocks > 0 ? gather(id0, 0) : 0u;
+
+  f32x4 acc[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY;  // reference max (log2 units) of this lane's head over this wave's keys
+  float l_run = 0.f;        // this lane's share of the sum
+  const float c_log2 = p.scale_log2;
+  // MFMA rows 4g..4g+3 of S^T are keys key_of_row(4g + i)
+  int kor[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) kor[i] = key_of_row(4 * g + i);
+  // QK operand rows: MFMA row r16 is key key_of_row(r16)
+  const int qrow = key_of_row(r16);
+  // transposing V^T reads: lanes 4j..4j+3 of group g point at key
+  // key_of_row(4g + j), 8-byte piece (lane & 3) of the feature block
+  const int vrow = key_of_row(4 * g + (r16 >> 2));
+  const int voff = vrow * kCkvPitch + (r16 & 3) * 8;
+
+  for (int j = 0; j < my_blocks; ++j) {
+    const int st = j & 1;
+    const uint32_t vmask = vm_next;
+    // the next block goes to the other stage (its block j-1 was consumed in
+    // the previous iteration: every LDS read of it has completed)
+    if (j + 1 < my_blocks) {
+      vm_next = gather(my_ids[(j + 1) * kWaveBlock + r16], st ^ 1);
+      wait_vmcnt<18>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    const char *stg = ring + st * kWaveStage;
+
+    // ---- S^T of the block (two accumulation chains)
+    // (all 18 operand reads are issued before the first MFMA, so they cost
+    // one LDS round trip, not one each)
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+    {
+      const char *rowp = stg + qrow * kCkvPitch + g * 16;
+      const char *kp = stg + kWaveKpeOff + qrow * 16 + g * 256;
+      bf16x8 ka[18];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) ka[k] = *(const bf16x8 *)(rowp + k * 64);
+      ka[16] = *(const bf16x8 *)kp;
+      ka[17] = *(const bf16x8 *)(kp + 1024);
+#pragma unroll
+      for (int k = 0; k < 18; k += 2) {
+        s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[k], q[k], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[k + 1], q[k + 1], s1, 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, 18, 0);  // DS reads
+      __builtin_amdgcn_sched_group_barrier(0x008, 18, 0);  // then the MFMAs
+    }
+    const f32x4 s = s0 + s1;
+
+    // ---- online softmax (log2 domain, reference max moved lazily)
+    float d[4];
+    bool over = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool ok = (vmask >> kor[i]) & 1u;
+      d[i] = ok ? __builtin_fmaf(s[i], c_log2, -m_run) : -INFINITY;
+      over |= d[i] > kRescaleSlack;
+    }
+    if (__ballot(over) != 0) {  // wave-uniform, rare after the first block
+      float mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if ((vmask >> kor[i]) & 1u) mx = fmaxf(mx, s[i] * c_log2);
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int fb = 0; fb < 32; ++fb) acc[fb] *= alpha;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool ok = (vmask >> kor[i]) & 1u;
+        d[i] = ok ? __builtin_fmaf(s[i], c_log2, -m_run) : -INFINITY;
+      }
+    }
+    bf16x4 p_hi, p_lo;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float pv = fast_exp2(d[i]);
+      l_run += pv;
+      p_hi[i] = (__bf16)pv;
+      p_lo[i] = (__bf16)(pv - (float)p_hi[i]);
+    }
+    const i16x4 ph = __builtin_bit_cast(i16x4, p_hi), pl = __builtin_bit_cast(i16x4, p_lo);
+
+    // ---- O^T += V^T . P^T in four batches of eight feature blocks: the
+    // transposing reads of batch b+1 are issued before batch b's MFMAs
+    const uint32_t va = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)(stg + voff);
+    auto pv8 = [&](int f0, const u32x2 (&v)[8]) {
+#pragma unroll
+      for (int f = 0; f < 8; ++f) {
+        const i16x4 a = __builtin_bit_cast(i16x4, v[f]);
+        const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, ph, acc[f0 + f], 0, 0, 0);
+        acc[f0 + f] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pl, c, 0, 0, 0);
+      }
+    };
+    u32x2 b0[8], b1[8], b2[8], b3[8];
+    tr_issue8<0>(va, b0);
+    tr_issue8_wait<8>(va, b1, b0);
+    pv8(0, b0);
+    tr_issue8_wait<16>(va, b2, b1);
+    pv8(8, b1);
+    tr_issue8_wait<24>(va, b3, b2);
+    pv8(16, b2);
+    tr_wait_all(b3);
+    pv8(24, b3);
+  }
+
+  // ---- merge the four waves' partials through LDS.  A wave's ring is free
+  // once its own loop is done, so each wave writes its (m, l) pairs and the
+  // unscaled feature blocks the other waves own into its own ring, and one
+  // barrier later every wave adds up its blocks in wave order.
+  l_run += __shfl_xor(l_run, 16);
+  l_run += __shfl_xor(l_run, 32);
+  // in ring(src): the 8 KB slice for wave dst at slot (dst - (dst > src)),
+  // lane order (1 KB per feature block), then 16 (m, l) pairs
+  auto slice = [&](int src, int dst) -> f32x4 * {
+    return (f32x4 *)(lds + src * kWaveRing + (dst - (dst > src)) * 8192);
+  };
+  auto pairs = [&](int src) -> float2 * { return (float2 *)(lds + src * kWaveRing + 3 * 8192); };
+  if (lane < 16) pairs(wave)[lane] = make_float2(m_run, l_run);
+#pragma unroll
+  for (int dst = 0; dst < kWaveWaves; ++dst) {
+    if (dst == wave) continue;
+    f32x4 *sl = slice(wave, dst);
+#pragma unroll
+    for (int f = 0; f < 8; ++f) sl[f * 64 + lane] = acc[dst * 8 + f];
+  }
+  lds_barrier();
+  float M = -INFINITY;
+  float mw[kWaveWaves], lw[kWaveWaves];
+#pragma unroll
+  for (int w = 0; w < kWaveWaves; ++w) {
+    const float2 v = pairs(w)[r16];
+    mw[w] = v.x;
+    lw[w] = v.y;
+    M = fmaxf(M, v.x);
+  }
+  float L = 0.f, aw[kWaveWaves];
+#pragma unroll
+  for (int w = 0; w < kWaveWaves; ++w) {
+    aw[w] = (mw[w] == -INFINITY) ? 0.f : fast_exp2(mw[w] - M);
+    L += aw[w] * lw[w];
+  }
+  // this wave's own blocks (static register indices: one uniform branch per wave)
+  f32x4 mine[8];
+#pragma unroll
+  for (int w = 0; w < kWaveWaves; ++w)
+    if (w == wave) {
+#pragma unroll
+      for (int f = 0; f < 8; ++f) mine[f] = acc[w * 8 + f];
+    }
+  f32x4 o[8];
+#pragma unroll
+  for (int f = 0; f < 8; ++f) o[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int w = 0; w < kWaveWaves; ++w) {  // wave order: deterministic sums
+#pragma unroll
+    for (int f = 0; f < 8; ++f) o[f] += aw[w] * ((w == wave) ? mine[f] : slice(w, wave)[f * 64 + lane]);
+  }
+
+  if (p.num_splits == 1 && !p.partial_only) {
+    const float inv = (M == -INFINITY) ? 0.f : 1.f / L;
+#pragma unroll
+    for (int f = 0; f < 8; ++f) {
+      const int f0 = (wave * 8 + f) * 16 + 4 * g;
       bf16x4 ob;
 #pragma unroll
       for (int k = 0; k < 4; ++k) ob[k] = (__bf16)(o[f][k] * inv);
       *(bf16x4 *)(p.out + t * p.out_st + head * p.out_sh + f0 * 2) = ob;
     }
+    if (wave == 0 && lane < 16)
+      p.lse[t * p.lse_st + head * p.lse_sh] = (M == -INFINITY) ? -INFINITY : M + __log2f(L);
+    return;
   }
-  if (fs == 0 && lane < 16)
-    p.lse[t * p.lse_st + head * p.lse_sh] = (M == -INFINITY) ? -INFINITY : M + __log2f(L);
-  }
+  split_partial<kWaveWaves, 8>(p, t, split, head, wave, lane, wave, o, M, L, wave == 0);
 }
 
 // Log-sum-exp merge of the per-chunk partials (reference: dsa_reduce_kernel,
@@ -977,6 +1298,15 @@ hipError_t launch_ring(const AttnParams &p, int head_blocks, hipStream_t stream)
   return hipGetLastError();
 }
 
+hipError_t launch_wave(const AttnParams &p, int head_blocks, hipStream_t stream) {
+  const dim3 grid(p.T * p.num_splits, head_blocks), block(kWaveWaves * 64);
+  if (p.narrow)
+    hipLaunchKernelGGL(dsa_attn_wave_kernel<true>, grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL(dsa_attn_wave_kernel<false>, grid, block, 0, stream, p);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 bool attn_merges_in_kernel(int H) { return (H / kHeadsPerGroup) % 2 != 0; }  // the <8, 8> layout
@@ -1001,7 +1331,7 @@ hipError_t launch_attention_partial(const AttnParams &p, hipStream_t stream) {
   if (groups % 8 == 0) return launch_ring<8, 1>(p, hb, stream);  // one wave per head group
   if (groups % 4 == 0) return launch_ring<4, 1>(p, hb, stream);
   if (groups % 2 == 0) return launch_ring<8, 4>(p, hb, stream);  // 2 groups x 4 slices
-  return launch_ring<8, 8>(p, hb, stream);                       // 1 group x 8 slices
+  return launch_wave(p, hb, stream);                             // 1 group, 4 independent waves
 }
 
 hipError_t launch_attention_merge(const AttnParams &p, hipStream_t stream) {
