@@ -32,7 +32,9 @@ HEAD_DIM_KPE = 64
 
 
 def _stream_handle(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The current HIP stream of ``device`` as a raw handle (an int)."""
+    return torch._C._cuda_getCurrentRawStream(device.index if device.index is not None
+                                              else torch.cuda.current_device())
 
 
 def new_workspace(q_nope: torch.Tensor, topk: int, num_splits: int = 0) -> torch.Tensor:
@@ -169,10 +171,114 @@ def _attn_args(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, num
     return a, (q_nope, q_pe, ckv, kpe, idx), T, H, K, dev
 
 
+# Validated call shapes of the value-returning entry points: a call whose
+# tensors have the shapes, strides, dtypes and devices of an earlier one (and
+# the same scale and split request) reuses that call's checked argument
+# struct and size queries and only sets the data pointers, so an eager call
+# costs little more than the launch.  Calls whose tensors would need a copy
+# (a non-contiguous last dimension) always take the checked path.
+class _Plan:
+    __slots__ = ("template", "T", "H", "dev", "ws_bytes", "c_bytes")
+
+
+_plans = {}
+_PLAN_LIMIT = 256
+
+# Workspaces of eager calls that bring none, one grow-only buffer per (device,
+# stream): calls of one stream run one after another, and a workspace's
+# contents do not matter.  Calls under graph capture take theirs from the
+# graph's memory pool instead.
+_stream_workspaces = {}
+
+
+def _plan_key(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, num_splits):
+    return (q_nope.shape, q_nope.stride(), q_nope.dtype, q_nope.get_device(),
+            q_pe.shape, q_pe.stride(), q_pe.dtype, q_pe.get_device(),
+            ckv_cache.shape, ckv_cache.stride(), ckv_cache.dtype, ckv_cache.get_device(),
+            kpe_cache.shape, kpe_cache.stride(), kpe_cache.dtype, kpe_cache.get_device(),
+            sparse_indices.shape, sparse_indices.stride(), sparse_indices.dtype,
+            sparse_indices.get_device(), sm_scale, num_splits)
+
+
+def _make_plan(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, num_splits):
+    """Checks the call (raising as the checked path does) and returns its
+    plan, or None when a tensor would need a copy."""
+    a, keep, T, H, K, dev = _attn_args(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices,
+                                       sm_scale, num_splits)
+    if any(x.data_ptr() != y.data_ptr() for x, y in
+           zip(keep, (q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices))):
+        return None
+    lib = _lib.load()
+    plan = _Plan()
+    a.out_stride_t, a.out_stride_h = H * HEAD_DIM_CKV, HEAD_DIM_CKV
+    a.lse_stride_t, a.lse_stride_h = H, 1
+    plan.template = bytes(a)
+    plan.T, plan.H, plan.dev = T, H, dev
+    plan.ws_bytes = lib.dsa_attn_workspace_bytes(T, H, K, int(num_splits))
+    plan.c_bytes = lib.dsa_attn_counter_bytes(T, H) if plan.ws_bytes else 0
+    return plan
+
+
+def _stream_workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    key = (dev.index, stream)
+    buf = _stream_workspaces.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 2 * buf.numel() if buf is not None else 0),
+                          dtype=torch.uint8, device=dev)
+        _stream_workspaces[key] = buf
+    return buf
+
+
+def _attention_planned(plan, q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices):
+    a = _lib.AttnArgs.from_buffer_copy(plan.template)
+    a.q_nope, a.q_pe = q_nope.data_ptr(), q_pe.data_ptr()
+    a.ckv, a.kpe, a.sparse_indices = ckv_cache.data_ptr(), kpe_cache.data_ptr(), sparse_indices.data_ptr()
+    dev = plan.dev
+    output = torch.empty((plan.T, plan.H, HEAD_DIM_CKV), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((plan.T, plan.H), dtype=torch.float32, device=dev)
+    a.output, a.lse = output.data_ptr(), lse.data_ptr()
+    stream = _stream_handle(dev)
+    cnt = None
+    if plan.ws_bytes:
+        if torch.cuda.is_current_stream_capturing():
+            ws = torch.empty(plan.ws_bytes, dtype=torch.uint8, device=dev)
+        else:
+            ws = _stream_workspace(dev, stream, plan.ws_bytes)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+        if plan.c_bytes:
+            cnt = _default_counters(dev, plan.c_bytes)
+            if cnt is not None:
+                a.split_counters, a.split_counters_bytes = cnt.data_ptr(), cnt.numel() * 4
+    lib = _lib.load()
+    rc = lib.dsa_attn_fwd(ctypes.byref(a), stream)
+    if rc != _lib.DSA_OK and cnt is not None:
+        _rezero_counters(cnt)
+    _lib.check("dsa_attn_fwd", rc)
+    return output, lse
+
+
 def _attention(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, num_splits: int,
                output: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
                workspace: Optional[torch.Tensor] = None,
                split_counters: Optional[torch.Tensor] = None):
+    if (output is None and lse is None and workspace is None and split_counters is None
+            and isinstance(sm_scale, (int, float))):
+        try:
+            key = _plan_key(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale,
+                            num_splits)
+        except (AttributeError, TypeError):
+            key = None  # not tensors: the checked path below raises
+        if key is not None:
+            plan = _plans.get(key)
+            if plan is None:
+                plan = _make_plan(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale,
+                                  num_splits)
+                if plan is not None:
+                    if len(_plans) >= _PLAN_LIMIT:
+                        _plans.clear()
+                    _plans[key] = plan
+            if plan is not None:
+                return _attention_planned(plan, q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices)
     a, keep, T, H, K, dev = _attn_args(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices,
                                        sm_scale, num_splits)
     if output is None:
