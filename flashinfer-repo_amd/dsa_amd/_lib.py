@@ -9,7 +9,10 @@ from __future__ import annotations
 import ctypes
 import os
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libdsa_amd.so")
+# DSA_AMD_LIB names another build of the same ABI (e.g. libdsa_amd_san.so,
+# the sanitizer build the CPU ABI tests run against).
+LIB_PATH = os.environ.get("DSA_AMD_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                                         "libdsa_amd.so")
 
 DSA_OK = 0
 DSA_EINVAL = 1
