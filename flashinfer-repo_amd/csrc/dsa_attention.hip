@@ -865,11 +865,12 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
 //
 // Per block (16 keys):
 //   S^T[16 keys x 16 heads] = K[keys x 576] . Q^T   18 x MFMA 16x16x32 bf16
-//   O^T[512 x 16 heads]    += V^T[512 x keys] . P^T 32 x 2 x MFMA 16x16x16 bf16
-// (P in bf16 hi + lo parts).  MFMA row m of S^T is key key_of_row(m); the D
-// layout of S^T (lane 16g + c: rows 4g..4g+3 of head c) is the B-operand
-// layout of P^T for the 16x16x16 product, whose A operand (V^T, features x
-// keys 4g..4g+3) is one ds_read_b64_tr_b16 per feature block.
+//   O^T[512 x 16 heads]    += V^T[512 x keys] . P^T 32 x MFMA 16x16x32 bf16
+// (P in bf16 hi + lo parts, both in one product: k-slots 8g..8g+3 hi,
+// 8g+4..8g+7 lo).  MFMA row m of S^T is key key_of_row(m); the D layout of
+// S^T (lane 16g + c: rows 4g..4g+3 of head c) gives lane group g the P^T
+// values of key rows 4g..4g+3, whose V^T values (the A operand, repeated for
+// the lo slots) are one ds_read_b64_tr_b16 per feature block.
 //
 // Stage layout: 16 ckv rows at a 1040-byte pitch (key k at row k), then the
 // 16 kpe rows chunk-major (16-byte chunk c of key k at 256 c + 16 k), so the
@@ -1137,17 +1138,22 @@ __global__ __launch_bounds__(kWaveWaves * 64, 1) void dsa_attn_wave_kernel(AttnP
       p_hi[i] = (__bf16)pv;
       p_lo[i] = (__bf16)(pv - (float)p_hi[i]);
     }
-    const i16x4 ph = __builtin_bit_cast(i16x4, p_hi), pl = __builtin_bit_cast(i16x4, p_lo);
+    // P^T as one 16x16x32 B operand: k-slots 8g .. 8g+3 of lane group g
+    // hold the hi parts of key rows 4g .. 4g+3, k-slots 8g+4 .. 8g+7 their lo
+    // parts, so P = hi + lo costs one MFMA per feature block (a 16x16x16
+    // product takes as many cycles as a 16x16x32 one).
+    const bf16x8 pb = __builtin_shufflevector(p_hi, p_lo, 0, 1, 2, 3, 4, 5, 6, 7);
 
     // ---- O^T += V^T . P^T in four batches of eight feature blocks: the
-    // transposing reads of batch b+1 are issued before batch b's MFMAs
+    // transposing reads of batch b+1 are issued before batch b's MFMAs.  The
+    // A operand repeats the four V^T values of key rows 4g .. 4g+3 for the
+    // lo k-slots.
     const uint32_t va = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)(stg + voff);
     auto pv8 = [&](int f0, const u32x2 (&v)[8]) {
 #pragma unroll
       for (int f = 0; f < 8; ++f) {
-        const i16x4 a = __builtin_bit_cast(i16x4, v[f]);
-        const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, ph, acc[f0 + f], 0, 0, 0);
-        acc[f0 + f] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pl, c, 0, 0, 0);
+        const bf16x8 a = __builtin_bit_cast(bf16x8, u32x4{v[f][0], v[f][1], v[f][0], v[f][1]});
+        acc[f0 + f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, acc[f0 + f], 0, 0, 0);
       }
     };
     u32x2 b0[8], b1[8], b2[8], b3[8];
