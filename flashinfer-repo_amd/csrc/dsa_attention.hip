@@ -324,6 +324,85 @@ __device__ __forceinline__ f32x4 qk_part(int part, const char *rowp, const char 
   return kChains == 2 ? c[0] + c[1] : c[0];
 }
 
+// Fused QK/PV loop (one-slice layouts, one head group per wave): S^T of
+// both 16-key blocks of tile i interleaved with the PV product of tile i-1.
+// Step K (0..35) is QK k-step K % 18 of key block K / 18 and, for K < 32,
+// feature block K of the PV product (its V^T halves of key block 0 and 1).
+// The reads of step K+1 are issued before the MFMAs of step K, so a step's
+// LDS latency is covered by the previous step's MFMAs (1 QK + 2 PV), and
+// consecutive MFMAs of one chain are never back to back.  qa*/ka*: LDS
+// addresses of this lane's QK operand rows (ckv; kpe + 128 g) of key blocks
+// 0 and 1; va: the V^T read address (as in the pv stage).
+struct FusedAddr {
+  uint32_t qa0, qa1, ka0, ka1, va;
+};
+
+template <int K>
+__device__ __forceinline__ void fused_issue(const FusedAddr &a, u32x4 &kq, u32x2 (&vt)[2]) {
+  constexpr int kRowB = 16 * kCkvPitch;  // key block 1 of the V^T reads
+  constexpr int kStep = K % 18;
+  constexpr int kOff = kStep < 16 ? kStep * 64 : (kStep - 16) * 512;
+  const uint32_t qa = K < 18 ? (kStep < 16 ? a.qa0 : a.ka0) : (kStep < 16 ? a.qa1 : a.ka1);
+  if constexpr (K < 32) {
+    asm volatile(
+        "ds_read_b128 %0, %3 offset:%4\n\t"
+        "ds_read_b64_tr_b16 %1, %5 offset:%6\n\t"
+        "ds_read_b64_tr_b16 %2, %5 offset:%7"
+        : "=&v"(kq), "=&v"(vt[0]), "=&v"(vt[1])
+        : "v"(qa), "i"(kOff), "v"(a.va), "i"(K * 32), "i"(kRowB + K * 32)
+        : "memory");
+  } else {
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=&v"(kq) : "v"(qa), "i"(kOff) : "memory");
+  }
+}
+
+// Waits until at most N LDS operations issued after step K's reads are
+// outstanding (LDS operations complete in issue order; any other operation
+// counted meanwhile only makes the wait longer).  Step K's registers are
+// in/out operands, so their uses cannot move above the wait.
+template <int N, int K>
+__device__ __forceinline__ void fused_wait(u32x4 &kq, u32x2 (&vt)[2]) {
+  if constexpr (K < 32)
+    asm volatile("s_waitcnt lgkmcnt(%3)" : "+v"(kq), "+v"(vt[0]), "+v"(vt[1]) : "n"(N) : "memory");
+  else
+    asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(kq) : "n"(N) : "memory");
+}
+
+template <int K = 0>
+__device__ __forceinline__ void qk_pv_steps(const FusedAddr &a, const QkOperands<1> &q, const bf16x8 &p_hi,
+                                            const bf16x8 &p_lo, f32x4 (&acc)[32], f32x4 (&s)[2],
+                                            u32x4 (&kq)[2], u32x2 (&vt)[2][2]) {
+  if constexpr (K < 36) {
+    constexpr int kNext = K + 1;
+    if constexpr (kNext < 36) fused_issue<kNext>(a, kq[kNext & 1], vt[kNext & 1]);
+    constexpr int kAfter = kNext < 36 ? (kNext < 32 ? 3 : 1) : 0;
+    fused_wait<kAfter, K>(kq[K & 1], vt[K & 1]);
+    constexpr int kStep = K % 18;
+    const bf16x8 b = kStep < 16 ? q.nope[kStep] : q.pe32[kStep - 16];
+    const bf16x8 ak = __builtin_bit_cast(bf16x8, kq[K & 1]);
+    if constexpr (K < 32) {
+      const bf16x8 av = __builtin_bit_cast(bf16x8, u32x4{vt[K & 1][0][0], vt[K & 1][0][1], vt[K & 1][1][0],
+                                                         vt[K & 1][1][1]});
+      acc[K] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, p_hi, acc[K], 0, 0, 0);
+      s[K / 18] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, b, s[K / 18], 0, 0, 0);
+      acc[K] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, p_lo, acc[K], 0, 0, 0);
+    } else {
+      s[K / 18] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, b, s[K / 18], 0, 0, 0);
+    }
+    qk_pv_steps<K + 1>(a, q, p_hi, p_lo, acc, s, kq, vt);
+  }
+}
+
+__device__ __forceinline__ void qk_pv_tile(const FusedAddr &a, const QkOperands<1> &q, const bf16x8 &p_hi,
+                                           const bf16x8 &p_lo, f32x4 (&acc)[32], f32x4 (&s)[2]) {
+  u32x4 kq[2];
+  u32x2 vt[2][2];
+  s[0] = f32x4{0.f, 0.f, 0.f, 0.f};
+  s[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  fused_issue<0>(a, kq[0], vt[0]);
+  qk_pv_steps(a, q, p_hi, p_lo, acc, s, kq, vt);
+}
+
 // Source of one wave's share of a tile gather (see tile_src in the kernel).
 template <int ROWS>
 struct GatherSrc {
@@ -548,6 +627,14 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
     }
   }
 
+  // The fused QK/PV loop of the one-slice layouts runs a PV step on the
+  // first tile too, from the stage of tile -1 with zero probabilities: that
+  // stage's ckv rows are zeroed here (its first gather is issued after the
+  // first tile is computed), so the step adds exact zeros.
+  if constexpr (FS == 1) {
+    u32x4 *z = (u32x4 *)(lds + (kStages - 1) * kStageBytes);
+    for (int i = threadIdx.x; i < kCkvStageBytes / 16; i += W * 64) z[i] = u32x4{0u, 0u, 0u, 0u};
+  }
   // Retire the Q loads with a wait the compiler sees (s_waitcnt vmcnt(0)), so
   // its own bookkeeping has nothing outstanding when the gather ring starts
   // and it adds no drain at the loop header.
@@ -736,7 +823,10 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
     });
   };
 
-  const int pre = min(n_tiles, kStages - 1);
+  // two teams of waves (W == 8, one-slice): waves 0-3 and 4-7, one of each
+  // per SIMD, half an iteration apart (below); they keep two tiles ahead
+  constexpr bool kTeams = FS == 1 && W == 8;
+  const int pre = min(n_tiles, kTeams ? 2 : kStages - 1);
   for (int j = 0; j < pre; ++j) fire_tile(j, tile_src(j));
 
   // the first ring pass's tile masks, built while the first tiles are in flight
@@ -767,50 +857,125 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
   // longer, which is what the fourth stage is for; two tiles remain in
   // flight.
   bf16x8 p_hi = {}, p_lo = {};
-  int next_refill = 16;  // the next tile index whose issue triggers a slot-id refill
-  for (int i = 0; i < n_tiles; ++i) {
-    wait_tile(i);
-    __builtin_amdgcn_s_barrier();  // every wave's share of tile i landed
-    // stage offsets: tile i, and tile i-1 (whose stage receives tile i+3)
-    const int st_cur = (i & (kStages - 1)) * kStageBytes;
-    const int st_prev = ((i + kStages - 1) & (kStages - 1)) * kStageBytes;
-    const char *st_ckv = lds + st_cur;
-    f32x4 sacc[2];
-    scores(st_ckv, sacc);
-    if (i > 0) pv(lds + st_prev, p_hi, p_lo);
-    if (FS >= 2) xput(sacc[0]);
-    // (The one-slice layouts compute the addresses after the barrier: their
-    // waves have no registers to hold them across it.)
-    const bool refill_stage = i + kStages - 1 < n_tiles;
-    TileSrc nxt;
-    if (FS >= 2 && refill_stage) nxt = tile_src(i + kStages - 1);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): partial written, tile i-1 read
-    __builtin_amdgcn_s_barrier();
-    if (FS == 1 && refill_stage) nxt = tile_src(i + kStages - 1);
-    if (refill_stage) fire_tile(i + kStages - 1, nxt);
-    // Ring refill (layouts whose ring holds 32 tiles' ids): once tile J = 16 m
-    // (m >= 1) is issued, every wave has passed a barrier since it read the
-    // ids of tiles J - 16 .. J - 1, so their half of the ring takes the ids of
-    // tiles J + 16 .. J + 31 (one 4-byte DMA per lane; raw ids, checked when
-    // issued).  The DMA completes before the loads of tile J + 1 (in-order
-    // vmcnt) and is visible after that tile's barrier, 14 iterations before
-    // tile J + 16 is issued.  The stage waits meanwhile count one extra load,
-    // which only makes them wait longer.
-    if constexpr (FS >= 2) {
-      static_assert(W == 8, "a half refill is 512 ids, one per lane of 8 waves");
-      const int J = i + kStages - 1;
-      if (J == next_refill) {  // J = 16, 32, ... (kept in a scalar, not tested per tile)
-        next_refill += 16;
-        if (J + 16 < n_tiles) {
-          const int key = (J + 16) * kKeysPerTile + wave * 64 + lane;  // W == 8: 512 keys
-          const int32_t *src = key < n_keys ? p.idx + (int64_t)t * p.idx_st + k_begin + key
-                                            : g_minus_one + lane;
-          lds_dma4(src, slots + ((J + 16) % L::kRingTiles) * kKeysPerTile + wave * 64);
-        }
+  auto lds_addr = [](const char *q) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)q;
+  };
+  const int k0 = key_of_row(r16), k1 = 16 + key_of_row(r16);
+  if constexpr (kTeams) {
+    const bool team_b = wave >= 4;
+    f32x4 sb[2];  // S^T of the wave's current tile, from its QK/PV step to its softmax
+    auto fused = [&](int i, f32x4 (&sacc)[2]) {
+      const char *st_ckv = lds + (i & (kStages - 1)) * kStageBytes;
+      const char *st_prev = lds + ((i + kStages - 1) & (kStages - 1)) * kStageBytes;
+      const char *st_kpe = st_ckv + kCkvStageBytes;
+      const FusedAddr fa = {
+          lds_addr(st_ckv + k0 * kCkvPitch + g * 16), lds_addr(st_ckv + k1 * kCkvPitch + g * 16),
+          lds_addr(st_kpe + (k0 >> 3) * kKpeGroupPitch + (k0 & 7) * 16 + g * 128),
+          lds_addr(st_kpe + (k1 >> 3) * kKpeGroupPitch + (k1 & 7) * 16 + g * 128),
+          lds_addr(st_prev + (kbase + 2 * (r16 >> 2)) * kCkvPitch + 4 * (r16 & 3) * 2)};
+      qk_pv_tile(fa, qreg, p_hi, p_lo, acc, sacc);
+    };
+    // Both teams run the same loop (X_j, fused j, Y_j, softmax j); team B
+    // passes one extra barrier first and team A one after, so the barriers
+    // pair A's X_j with B's Y_{j-1} and A's Y_j with B's X_j: each team's
+    // QK/PV of a tile runs while the other team does its softmax.  Before a
+    // barrier that lets either team compute tile j, both teams' shares of
+    // tile j have landed: A waits before X_j, B before Y_{j-1}.  The stage of
+    // tile j-2 is free once both teams passed their fused step j-1: at the
+    // pair (A's X_j, B's Y_{j-1}), where both fire their shares of tile j+2.
+    int fired = pre - 1;  // last tile whose share this wave has issued
+    auto wait_own = [&](int j) {  // this wave's share of tile j landed
+      const int ahead = fired - j;
+      if (ahead >= 2)
+        wait_vmcnt<2 * R::kLoads>();
+      else if (ahead == 1)
+        wait_vmcnt<R::kLoads>();
+      else
+        wait_vmcnt<0>();
+    };
+    if (team_b) {
+      __builtin_amdgcn_s_barrier();
+      if (2 < n_tiles) {
+        fire_tile(2, tile_src(2));
+        fired = 2;
       }
     }
-    if (FS >= 2) reduce(sacc);
-    softmax(sacc, __builtin_amdgcn_readlane(tile_masks, i), p_hi, p_lo);
+    for (int j = 0; j < n_tiles; ++j) {
+      wait_own(j);
+      __builtin_amdgcn_s_barrier();  // X_j
+      if (!team_b && j + 2 < n_tiles) {
+        fire_tile(j + 2, tile_src(j + 2));
+        fired = j + 2;
+      }
+      fused(j, sb);
+      if (team_b && j + 1 < n_tiles) wait_own(j + 1);
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      __builtin_amdgcn_s_barrier();  // Y_j
+      if (team_b && j + 3 < n_tiles) {
+        fire_tile(j + 3, tile_src(j + 3));
+        fired = j + 3;
+      }
+      softmax(sb, __builtin_amdgcn_readlane(tile_masks, j), p_hi, p_lo);
+    }
+    if (!team_b) __builtin_amdgcn_s_barrier();
+  } else {
+    int next_refill = 16;  // the next tile index whose issue triggers a slot-id refill
+    for (int i = 0; i < n_tiles; ++i) {
+      wait_tile(i);
+      __builtin_amdgcn_s_barrier();  // every wave's share of tile i landed
+      // stage offsets: tile i, and tile i-1 (whose stage receives tile i+3)
+      const int st_cur = (i & (kStages - 1)) * kStageBytes;
+      const int st_prev = ((i + kStages - 1) & (kStages - 1)) * kStageBytes;
+      const char *st_ckv = lds + st_cur;
+      f32x4 sacc[2];
+      if constexpr (FS == 1) {
+        // S^T of tile i fused with the PV product of tile i-1 (tile 0: the PV
+        // part reads the zeroed stage with zero probabilities)
+        const char *st_kpe = st_ckv + kCkvStageBytes;
+        const FusedAddr fa = {
+            lds_addr(st_ckv + k0 * kCkvPitch + g * 16), lds_addr(st_ckv + k1 * kCkvPitch + g * 16),
+            lds_addr(st_kpe + (k0 >> 3) * kKpeGroupPitch + (k0 & 7) * 16 + g * 128),
+            lds_addr(st_kpe + (k1 >> 3) * kKpeGroupPitch + (k1 & 7) * 16 + g * 128),
+            lds_addr(lds + st_prev + (kbase + 2 * (r16 >> 2)) * kCkvPitch + 4 * (r16 & 3) * 2)};
+        qk_pv_tile(fa, qreg, p_hi, p_lo, acc, sacc);
+      } else {
+        scores(st_ckv, sacc);
+        if (i > 0) pv(lds + st_prev, p_hi, p_lo);
+      }
+      if (FS >= 2) xput(sacc[0]);
+      // (The one-slice layouts compute the addresses after the barrier: their
+      // waves have no registers to hold them across it.)
+      const bool refill_stage = i + kStages - 1 < n_tiles;
+      TileSrc nxt;
+      if (FS >= 2 && refill_stage) nxt = tile_src(i + kStages - 1);
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): partial written, tile i-1 read
+      __builtin_amdgcn_s_barrier();
+      if (FS == 1 && refill_stage) nxt = tile_src(i + kStages - 1);
+      if (refill_stage) fire_tile(i + kStages - 1, nxt);
+      // Ring refill (layouts whose ring holds 32 tiles' ids): once tile J = 16 m
+      // (m >= 1) is issued, every wave has passed a barrier since it read the
+      // ids of tiles J - 16 .. J - 1, so their half of the ring takes the ids of
+      // tiles J + 16 .. J + 31 (one 4-byte DMA per lane; raw ids, checked when
+      // issued).  The DMA completes before the loads of tile J + 1 (in-order
+      // vmcnt) and is visible after that tile's barrier, 14 iterations before
+      // tile J + 16 is issued.  The stage waits meanwhile count one extra load,
+      // which only makes them wait longer.
+      if constexpr (FS >= 2) {
+        static_assert(W == 8, "a half refill is 512 ids, one per lane of 8 waves");
+        const int J = i + kStages - 1;
+        if (J == next_refill) {  // J = 16, 32, ... (kept in a scalar, not tested per tile)
+          next_refill += 16;
+          if (J + 16 < n_tiles) {
+            const int key = (J + 16) * kKeysPerTile + wave * 64 + lane;  // W == 8: 512 keys
+            const int32_t *src = key < n_keys ? p.idx + (int64_t)t * p.idx_st + k_begin + key
+                                              : g_minus_one + lane;
+            lds_dma4(src, slots + ((J + 16) % L::kRingTiles) * kKeysPerTile + wave * 64);
+          }
+        }
+      }
+      if (FS >= 2) reduce(sacc);
+      softmax(sacc, __builtin_amdgcn_readlane(tile_masks, i), p_hi, p_lo);
+    }
   }
   if (n_tiles > 0) pv(lds + ((n_tiles - 1) & (kStages - 1)) * kStageBytes, p_hi, p_lo);
 
