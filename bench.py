@@ -106,10 +106,10 @@ def csrc_hash() -> str:
     return h.hexdigest()
 
 
-def load_traffic(config: str):
-    """HBM bytes per launch of the dominant kernel from the committed rocprofv3
-    --pmc record (FETCH_SIZE + WRITE_SIZE, copy-calibrated), or None when no
-    record exists for this workload or it was made from other kernel sources."""
+def load_record(config: str):
+    """The committed rocprofv3 --pmc record of this workload's dominant kernel
+    (profiles/traffic.json), or None when none exists or it was made from
+    other kernel sources."""
     try:
         with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
             t = json.load(f)
@@ -118,7 +118,25 @@ def load_traffic(config: str):
     ent = t.get(config)
     if not ent or ent.get("csrc_sha256") != csrc_hash():
         return None
-    return ent.get("hbm_bytes_per_launch")
+    return ent
+
+
+def load_traffic(config: str):
+    """HBM bytes per launch of the dominant kernel (FETCH_SIZE + WRITE_SIZE,
+    copy-calibrated) from the record, or None."""
+    ent = load_record(config)
+    return ent.get("hbm_bytes_per_launch") if ent else None
+
+
+def load_counters(config: str):
+    """Counter-derived figures of the record: MFMA busy fraction
+    (SQ_VALU_MFMA_BUSY_CYCLES over 4 x SQ_BUSY_CU_CYCLES), L2 hit fraction
+    (TCC_HIT / (TCC_HIT + TCC_MISS)), fetched and written bytes; or None."""
+    ent = load_record(config)
+    if not ent:
+        return None
+    return {k: ent.get(k) for k in ("mfma_busy_frac", "l2_hit_frac", "fetch_bytes_per_launch",
+                                    "write_bytes_per_launch", "source")}
 
 
 def host_cpu():
@@ -260,15 +278,18 @@ def measure_attention(name, d, steps, warmup, cold_copies=0):
     # gather-attention launch is timed alone and the merge kernel is the rest.
     splits = num_splits(T, H, K)
     one_launch = splits == 1 or _lib.load().dsa_attn_counter_bytes(T, H) > 0
+    # H = 16 x an odd number: four independent waves per head group; else the
+    # shared-ring layout
+    kname = "dsa_attn_wave_kernel" if (H // 16) % 2 else "dsa_attn_ring_kernel"
     if one_launch:
         ms_dom = ms
-        kdesc = ("dsa_attn_ring_kernel (gather attention"
+        kdesc = (f"{kname} (gather attention"
                  + (" with the split merge inside" if splits > 1 else "")
                  + "; the only launch of a kernel() call)")
     else:
         ms_dom, _ = time_graph(graph_of(lambda: kernel_partial(*args, num_splits=0), per_graph),
                                per_graph, steps, warmup)
-        kdesc = "dsa_attn_ring_kernel (per-chunk gather attention; timed alone via dsa_attn_fwd_partial)"
+        kdesc = f"{kname} (per-chunk gather attention; timed alone via dsa_attn_fwd_partial)"
     eager_ms = time_eager(lambda: kernel(*args), steps)
 
     cold = None
@@ -294,10 +315,11 @@ def measure_attention(name, d, steps, warmup, cold_copies=0):
     tflops = alg_flops / (ms_dom * 1e-3) / 1e12
     hbm = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": load_traffic(name),
-           "algorithmic_bytes": alg_bytes, "kernel": kdesc}
+           "algorithmic_bytes": alg_bytes, "kernel": kdesc, "counters": load_counters(name)}
     mfma = {"bound": "mfma", "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 5),
-            "traffic": hbm["traffic"], "algorithmic_flops": alg_flops, "kernel": kdesc}
+            "traffic": hbm["traffic"], "algorithmic_flops": alg_flops, "kernel": kdesc,
+            "counters": hbm["counters"]}
     # Config 3 is the MFMA-bound shape by the target's definition (its gathers
     # hit a 40 MB causal window the caches hold); the others are priced
     # against HBM, with the MFMA fraction beside it.
@@ -363,7 +385,8 @@ def measure_indexer(steps, warmup):
                    "eager_pipeline_us": round(eager_ms * 1e3, 3)},
         "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS,
                      "unit": "TFLOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4),
-                     "traffic": load_traffic("cfg5"), "algorithmic_ops": ops,
+                     "traffic": load_traffic("cfg5"), "counters": load_counters("cfg5"),
+                     "algorithmic_ops": ops,
                      "kernel": "dsa_idx_prep_kernel + dsa_idx_score_kernel (timed via "
                                "dsa_indexer_topk with topk=0)"},
     }
