@@ -5,6 +5,7 @@
 // caller's stream.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <string>
@@ -35,12 +36,19 @@ bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+constexpr int64_t kMaxWaveSplits = 8;
+
 // Top-k chunk length per split and the split count that results.  Automatic
-// mode aims for about one workgroup per compute unit while keeping at least
-// four 32-key tiles per chunk; an explicit request is honoured up to one key
-// per split (the reference's kernel_splitk additionally required topk %
-// SPLIT_K == 0, kernel.py:512; uneven chunks are fine here).  Either way a
-// chunk never exceeds kMaxChunk entries, so very long rows get extra splits.
+// mode aims for about one workgroup per compute unit while keeping enough
+// work per chunk: four 32-key tiles for the shared-ring layouts; for the
+// four-wave layout (an odd number of 16-head groups) one 16-key block per
+// wave, and at most kMaxWaveSplits splits (measured at H=16, top-k 2048:
+// with 8 splits T = 1..16 run 1-3 us faster than with 16, whose longer
+// merge outweighs their parallelism; at T = 64, 4 splits).  An explicit
+// request is honoured up to one key per split (the reference's kernel_splitk
+// additionally required topk % SPLIT_K == 0, kernel.py:512; uneven chunks are
+// fine here).  Either way a chunk never exceeds the layout's maximum, so very
+// long rows get extra splits.
 void choose_splits(int64_t T, int64_t H, int64_t K, int32_t requested, int32_t *splits,
                    int32_t *chunk) {
   if (K <= 0) {
@@ -60,7 +68,9 @@ void choose_splits(int64_t T, int64_t H, int64_t K, int32_t requested, int32_t *
     const int64_t groups = H / dsa::kHeadsPerGroup > 0 ? H / dsa::kHeadsPerGroup : 1;
     const int64_t units = (T > 0 ? T : 1) * ceil_div(groups, 8);
     const int64_t tiles = ceil_div(K, dsa::kKeysPerTile);
-    const int64_t max_s = ceil_div(tiles, dsa::kMinTilesPerSplit);
+    const bool wave_layout = dsa::attn_merges_in_kernel((int)H);
+    const int64_t max_s = wave_layout ? std::min<int64_t>(ceil_div(K, 64), kMaxWaveSplits)
+                                      : ceil_div(tiles, dsa::kMinTilesPerSplit);
     S = ceil_div(dsa::kNumCU, units);
     if (S > max_s) S = max_s;
     if (S < min_s) S = min_s;

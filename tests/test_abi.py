@@ -66,7 +66,12 @@ def test_split_choice():
     assert lib.dsa_attn_num_splits(64, 128, 4096, 1) == 2      # ... and no longer
     assert lib.dsa_attn_num_splits(2048, 16, 1024, 0) == 1     # prefill needs no split
     assert lib.dsa_attn_num_splits(8, 16, 4096, 1) == 2        # requests below the minimum are raised
-    assert lib.dsa_attn_num_splits(1, 16, 2048, 0) == 16       # >= one tile per wave
+    # four-wave layout (H = 16 x odd): at most 8 splits, >= one 16-key block per wave
+    assert lib.dsa_attn_num_splits(1, 16, 2048, 0) == 8
+    assert lib.dsa_attn_num_splits(16, 16, 2048, 0) == 8
+    assert lib.dsa_attn_num_splits(4, 16, 256, 0) == 4          # 64 keys per split
+    assert lib.dsa_attn_num_splits(1, 16, 32768, 0) == 16       # 2048-key chunks at most
+    assert lib.dsa_attn_num_splits(1, 32, 2048, 0) == 16        # shared-ring layout: 4 tiles per split
     assert lib.dsa_attn_num_splits(64, 16, 2048, 16) == 16     # explicit request honoured
     assert lib.dsa_attn_num_splits(1, 16, 5, 128) == 5         # at most one key per split
     assert lib.dsa_attn_num_splits(4, 16, 0, 0) == 1
@@ -74,7 +79,7 @@ def test_split_choice():
     assert lib.dsa_attn_workspace_bytes(64, 16, 2048, 0) == 64 * 4 * 16 * (512 + 16) * 4
     assert lib.dsa_attn_workspace_bytes(256, 128, 2048, 2) == 256 * 2 * 128 * 528 * 4
     assert lib.dsa_attn_workspace_bytes(2048, 16, 1024, 0) == 0
-    # in-kernel merge (8-slice layout: odd numbers of 16-head groups): 8 wave
+    # in-kernel merge (four-wave layout: odd numbers of 16-head groups): 8 wave
     # counters per (token, workgroup along the heads); other layouts use none
     assert lib.dsa_attn_counter_bytes(64, 16) == 64 * 8 * 4
     assert lib.dsa_attn_counter_bytes(4, 48) == 4 * 3 * 8 * 4    # 3 groups, one workgroup each
