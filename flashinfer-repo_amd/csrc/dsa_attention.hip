@@ -1265,6 +1265,11 @@ __global__ __launch_bounds__(kWaveWaves * 64, 1) void dsa_attn_wave_kernel(AttnP
       __builtin_amdgcn_sched_group_barrier(0x100, 18, 0);  // DS reads
       __builtin_amdgcn_sched_group_barrier(0x008, 18, 0);  // then the MFMAs
     }
+    // the first batch of transposing V^T reads goes out now: its latency
+    // overlaps the softmax
+    const uint32_t va = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)(stg + voff);
+    u32x2 b0[8], b1[8], b2[8], b3[8];
+    tr_issue8<0>(va, b0);
     const f32x4 s = s0 + s1;
 
     // ---- online softmax (log2 domain, reference max moved lazily)
@@ -1313,7 +1318,6 @@ __global__ __launch_bounds__(kWaveWaves * 64, 1) void dsa_attn_wave_kernel(AttnP
     // transposing reads of batch b+1 are issued before batch b's MFMAs.  The
     // A operand repeats the four V^T values of key rows 4g .. 4g+3 for the
     // lo k-slots.
-    const uint32_t va = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)(stg + voff);
     auto pv8 = [&](int f0, const u32x2 (&v)[8]) {
 #pragma unroll
       for (int f = 0; f < 8; ++f) {
@@ -1321,8 +1325,6 @@ __global__ __launch_bounds__(kWaveWaves * 64, 1) void dsa_attn_wave_kernel(AttnP
         acc[f0 + f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, acc[f0 + f], 0, 0, 0);
       }
     };
-    u32x2 b0[8], b1[8], b2[8], b3[8];
-    tr_issue8<0>(va, b0);
     tr_issue8_wait<8>(va, b1, b0);
     pv8(0, b0);
     tr_issue8_wait<16>(va, b2, b1);
