@@ -228,21 +228,30 @@ def graph_of(fn, n):
     return graph
 
 
-def time_graph(graph, n_per, steps, warmup):
-    """ms per call: warm-up replays, then HIP events around the replays (on
-    the current stream, which the kernels run on)."""
+def time_graph(fn, steps, warmup, per=GRAPH_CALLS):
+    """ms per call over exactly `steps` calls of fn: HIP graphs of `per`
+    back-to-back calls (and one graph of the remainder when `per` does not
+    divide `steps`), warm-up replays, then HIP events around the replays (on
+    the current stream, which the kernels run on).  Returns (ms, steps)."""
     import torch
-    reps = max(1, -(-steps // n_per))
-    for _ in range(max(1, -(-warmup // n_per))):
-        graph.replay()
+    per = max(1, min(per, steps))
+    full, rest = divmod(steps, per)
+    g_full = graph_of(fn, per)
+    g_rest = graph_of(fn, rest) if rest else None
+    for _ in range(max(1, -(-warmup // per))):
+        g_full.replay()
+    if g_rest is not None:
+        g_rest.replay()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
-    for _ in range(reps):
-        graph.replay()
+    for _ in range(full):
+        g_full.replay()
+    if g_rest is not None:
+        g_rest.replay()
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / (reps * n_per), reps * n_per
+    return start.elapsed_time(end) / steps, steps
 
 
 def time_eager(fn, steps):
@@ -262,7 +271,8 @@ def measure_attention(name, d, steps, warmup, cold_copies=0):
     """Times kernel() on workload d; returns the fields of its line."""
     import torch
 
-    from dsa_amd import _lib, kernel, kernel_partial, num_splits, workloads
+    from dsa_amd import (_lib, kernel, kernel_out, kernel_partial, new_split_counters, new_workspace,
+                         num_splits, workloads)
     g = workloads.to_device(d, "cuda:0")
     T, H, _ = d["q_nope"].shape
     K = d["sparse_indices"].shape[1]
@@ -271,7 +281,7 @@ def measure_attention(name, d, steps, warmup, cold_copies=0):
     alg_bytes = workloads.attention_bytes(d["sparse_indices"])
     alg_flops = workloads.attention_flops(d["sparse_indices"], H)
     per_graph = min(GRAPH_CALLS, steps)
-    ms, timed = time_graph(graph_of(lambda: kernel(*args), per_graph), per_graph, steps, warmup)
+    ms, timed = time_graph(lambda: kernel(*args), steps, warmup)
 
     # The dominant kernel: a call of one launch (one chunk per token, or the
     # split merge inside the attention kernel) is that launch; otherwise the
@@ -287,10 +297,18 @@ def measure_attention(name, d, steps, warmup, cold_copies=0):
                  + (" with the split merge inside" if splits > 1 else "")
                  + "; the only launch of a kernel() call)")
     else:
-        ms_dom, _ = time_graph(graph_of(lambda: kernel_partial(*args, num_splits=0), per_graph),
-                               per_graph, steps, warmup)
+        ms_dom, _ = time_graph(lambda: kernel_partial(*args, num_splits=0), steps, warmup)
         kdesc = f"{kname} (per-chunk gather attention; timed alone via dsa_attn_fwd_partial)"
     eager_ms = time_eager(lambda: kernel(*args), steps)
+    # the same without allocation: the destination-passing entry with
+    # preallocated output, lse, workspace and split counters
+    out = torch.empty_like(g["q_nope"])
+    lse = torch.empty(g["q_nope"].shape[:2], dtype=torch.float32, device=g["q_nope"].device)
+    ws = new_workspace(g["q_nope"], K)
+    cnt = new_split_counters(g["q_nope"])
+    eager_dps_ms = time_eager(lambda: kernel_out(*args, out, lse, workspace=ws, split_counters=cnt),
+                              steps)
+    del out, lse, ws, cnt
 
     cold = None
     if cold_copies > 0:
@@ -303,7 +321,7 @@ def measure_attention(name, d, steps, warmup, cold_copies=0):
             kernel(g["q_nope"], g["q_pe"], c, k, g["sparse_indices"], d["sm_scale"])
 
         per = cold_copies * max(1, per_graph // cold_copies)
-        ms_cold, _ = time_graph(graph_of(cold_call, per), per, steps, warmup)
+        ms_cold, _ = time_graph(cold_call, steps, warmup, per)
         cold = {"copies": cold_copies,
                 "cache_bytes_per_copy": (g["ckv_cache"].numel() + g["kpe_cache"].numel()) * 2,
                 "us_per_call": round(ms_cold * 1e3, 3),
@@ -331,8 +349,10 @@ def measure_attention(name, d, steps, warmup, cold_copies=0):
         "config": {"workload": f"{name}: DSA sparse attention T={T} H={H} topk={K} "
                                f"ckv512+kpe64 bf16, {cache_slots} slots, page_size={ps}",
                    "tokens": T, "heads": H, "topk": K, "splits": splits,
-                   "timing": f"HIP graphs of {per_graph} back-to-back kernel() calls, replayed",
+                   "timing": f"HIP graphs of {per_graph} back-to-back kernel() calls, replayed "
+                             f"(plus one graph of the remainder): {steps} calls timed",
                    "eager_us_per_call": round(eager_ms * 1e3, 3),
+                   "eager_preallocated_us_per_call": round(eager_dps_ms * 1e3, 3),
                    "cold_cache": cold,
                    "launches_per_call": 1 if one_launch else 2,
                    "dominant_kernel_us": round(ms_dom * 1e3, 3),
@@ -367,9 +387,9 @@ def measure_indexer(steps, warmup):
         kernel(*attn, sl, d["sm_scale"])
 
     per_graph = min(GRAPH_CALLS, steps)
-    ms_idx, timed = time_graph(graph_of(indexer, per_graph), per_graph, steps, warmup)
-    ms_score, _ = time_graph(graph_of(scores_only, per_graph), per_graph, steps, warmup)
-    ms_pipe, _ = time_graph(graph_of(pipeline, per_graph), per_graph, steps, warmup)
+    ms_idx, timed = time_graph(indexer, steps, warmup)
+    ms_score, _ = time_graph(scores_only, steps, warmup)
+    ms_pipe, _ = time_graph(pipeline, steps, warmup)
     eager_ms = time_eager(pipeline, steps)
     ops = 2 * T * Hi * S * D                          # algorithmic dot-product ops
     tops = ops / (ms_score * 1e-3) / 1e12
@@ -377,7 +397,8 @@ def measure_indexer(steps, warmup):
         "us": ms_pipe * 1e3, "ms": ms_pipe, "timed": timed,
         "config": {"workload": f"cfg5: indexer T={T} heads={Hi} dim={D} positions={S} "
                                f"top-{K} -> block-table slots -> cfg2 attention H=16",
-                   "timing": f"HIP graphs of {per_graph} back-to-back calls, replayed",
+                   "timing": f"HIP graphs of {per_graph} back-to-back calls, replayed "
+                             f"(plus one graph of the remainder): {steps} calls timed",
                    "indexer_topk_us": round(ms_idx * 1e3, 3),
                    "score_kernels_us": round(ms_score * 1e3, 3),
                    "topk_kernel_us": round((ms_idx - ms_score) * 1e3, 3),

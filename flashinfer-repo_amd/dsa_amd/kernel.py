@@ -229,24 +229,65 @@ def _stream_workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tens
     return buf
 
 
-def _attention_planned(plan, q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices):
+def _check_output(output, T, H, dev):
+    _check(tuple(output.shape) == (T, H, HEAD_DIM_CKV) and output.dtype == torch.bfloat16
+           and output.stride(-1) == 1 and output.device == dev,
+           "output must be a [T, H, 512] bfloat16 tensor with a contiguous last dim")
+
+
+def _check_lse(lse, T, H, dev):
+    _check(tuple(lse.shape) == (T, H) and lse.dtype == torch.float32 and lse.device == dev,
+           "lse must be a [T, H] float32 tensor")
+
+
+def _check_workspace(workspace, ws_bytes, dev):
+    _check(workspace.device == dev and workspace.is_contiguous()
+           and workspace.numel() * workspace.element_size() >= ws_bytes,
+           f"workspace must be a contiguous tensor of >= {ws_bytes} bytes on {dev}")
+
+
+def _check_counters(split_counters, c_bytes, dev):
+    _check(split_counters.device == dev and split_counters.is_contiguous()
+           and split_counters.dtype == torch.int32
+           and split_counters.numel() * 4 >= c_bytes,
+           f"split_counters must be a contiguous int32 tensor of >= {c_bytes // 4} "
+           f"elements on {dev} (see new_split_counters)")
+
+
+def _attention_planned(plan, q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices,
+                       output=None, lse=None, workspace=None, split_counters=None):
     a = _lib.AttnArgs.from_buffer_copy(plan.template)
     a.q_nope, a.q_pe = q_nope.data_ptr(), q_pe.data_ptr()
     a.ckv, a.kpe, a.sparse_indices = ckv_cache.data_ptr(), kpe_cache.data_ptr(), sparse_indices.data_ptr()
     dev = plan.dev
-    output = torch.empty((plan.T, plan.H, HEAD_DIM_CKV), dtype=torch.bfloat16, device=dev)
-    lse = torch.empty((plan.T, plan.H), dtype=torch.float32, device=dev)
+    if output is None:
+        output = torch.empty((plan.T, plan.H, HEAD_DIM_CKV), dtype=torch.bfloat16, device=dev)
+    else:
+        _check_output(output, plan.T, plan.H, dev)
+        a.out_stride_t, a.out_stride_h = output.stride(0), output.stride(1)
+    if lse is None:
+        lse = torch.empty((plan.T, plan.H), dtype=torch.float32, device=dev)
+    else:
+        _check_lse(lse, plan.T, plan.H, dev)
+        a.lse_stride_t, a.lse_stride_h = lse.stride(0), lse.stride(1)
     a.output, a.lse = output.data_ptr(), lse.data_ptr()
     stream = _stream_handle(dev)
     cnt = None
     if plan.ws_bytes:
-        if torch.cuda.is_current_stream_capturing():
+        if workspace is not None:
+            _check_workspace(workspace, plan.ws_bytes, dev)
+            ws = workspace
+        elif torch.cuda.is_current_stream_capturing():
             ws = torch.empty(plan.ws_bytes, dtype=torch.uint8, device=dev)
         else:
             ws = _stream_workspace(dev, stream, plan.ws_bytes)
-        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * ws.element_size()
         if plan.c_bytes:
-            cnt = _default_counters(dev, plan.c_bytes)
+            if split_counters is not None:
+                _check_counters(split_counters, plan.c_bytes, dev)
+                cnt = split_counters
+            else:
+                cnt = _default_counters(dev, plan.c_bytes)
             if cnt is not None:
                 a.split_counters, a.split_counters_bytes = cnt.data_ptr(), cnt.numel() * 4
     lib = _lib.load()
@@ -261,8 +302,7 @@ def _attention(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, num
                output: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
                workspace: Optional[torch.Tensor] = None,
                split_counters: Optional[torch.Tensor] = None):
-    if (output is None and lse is None and workspace is None and split_counters is None
-            and isinstance(sm_scale, (int, float))):
+    if isinstance(sm_scale, (int, float)):
         try:
             key = _plan_key(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale,
                             num_splits)
@@ -278,26 +318,22 @@ def _attention(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, num
                         _plans.clear()
                     _plans[key] = plan
             if plan is not None:
-                return _attention_planned(plan, q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices)
+                return _attention_planned(plan, q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices,
+                                          output, lse, workspace, split_counters)
     a, keep, T, H, K, dev = _attn_args(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices,
                                        sm_scale, num_splits)
     if output is None:
         output = torch.empty((T, H, HEAD_DIM_CKV), dtype=torch.bfloat16, device=dev)
     if lse is None:
         lse = torch.empty((T, H), dtype=torch.float32, device=dev)
-    _check(tuple(output.shape) == (T, H, HEAD_DIM_CKV) and output.dtype == torch.bfloat16
-           and output.stride(-1) == 1 and output.device == dev,
-           "output must be a [T, H, 512] bfloat16 tensor with a contiguous last dim")
-    _check(tuple(lse.shape) == (T, H) and lse.dtype == torch.float32 and lse.device == dev,
-           "lse must be a [T, H] float32 tensor")
+    _check_output(output, T, H, dev)
+    _check_lse(lse, T, H, dev)
     lib = _lib.load()
     ws_bytes = lib.dsa_attn_workspace_bytes(T, H, K, int(num_splits))
     ws = None
     if ws_bytes:
         if workspace is not None:
-            _check(workspace.device == dev and workspace.is_contiguous()
-                   and workspace.numel() * workspace.element_size() >= ws_bytes,
-                   f"workspace must be a contiguous tensor of >= {ws_bytes} bytes on {dev}")
+            _check_workspace(workspace, ws_bytes, dev)
             ws = workspace
             ws_bytes = workspace.numel() * workspace.element_size()
         else:
@@ -309,11 +345,7 @@ def _attention(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, num
     c_bytes = lib.dsa_attn_counter_bytes(T, H) if ws is not None else 0
     if c_bytes:
         if split_counters is not None:
-            _check(split_counters.device == dev and split_counters.is_contiguous()
-                   and split_counters.dtype == torch.int32
-                   and split_counters.numel() * 4 >= c_bytes,
-                   f"split_counters must be a contiguous int32 tensor of >= {c_bytes // 4} "
-                   f"elements on {dev} (see new_split_counters)")
+            _check_counters(split_counters, c_bytes, dev)
             cnt = split_counters
         else:
             cnt = _default_counters(dev, c_bytes)
@@ -381,11 +413,8 @@ def kernel_noalloc(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale,
         _check(x.stride(-1) == 1, f"{name} must have a contiguous last dimension")
     a, keep, T, H, K, dev = _attn_args(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices,
                                        sm_scale, num_splits)
-    _check(tuple(output.shape) == (T, H, HEAD_DIM_CKV) and output.dtype == torch.bfloat16
-           and output.stride(-1) == 1 and output.device == dev,
-           "output must be a [T, H, 512] bfloat16 tensor with a contiguous last dim")
-    _check(tuple(lse.shape) == (T, H) and lse.dtype == torch.float32 and lse.device == dev,
-           "lse must be a [T, H] float32 tensor")
+    _check_output(output, T, H, dev)
+    _check_lse(lse, T, H, dev)
     a.output, a.out_stride_t, a.out_stride_h = output.data_ptr(), output.stride(0), output.stride(1)
     a.lse, a.lse_stride_t, a.lse_stride_h = lse.data_ptr(), lse.stride(0), lse.stride(1)
     lib = _lib.load()
