@@ -1041,6 +1041,29 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
 // 16 kpe rows chunk-major (16-byte chunk c of key k at 256 c + 16 k), so the
 // QK operand reads (16 rows, one column) and the transposing V^T reads (rows
 // key_of_row(4g + j)) are free of bank conflicts.
+// (token, chunk) of this workgroup.  Workgroups are dispatched to the eight
+// XCDs round robin (linear workgroup id mod 8), so the chunks of a token are
+// given ids of one residue mod 8: they share an XCD and its L2 (the token's Q
+// is fetched into one L2 instead of S, and the split exchange stays on one
+// XCD).  Tokens 8a .. T-1 (T = 8a + r) keep the plain order after them.  The
+// merge does not depend on this placement (its accesses are device
+// coherent); only the speed does.
+__device__ __forceinline__ void xcd_token_split(int T, int S, int &t, int &split) {
+  const int b = blockIdx.x;
+  const int grouped = (T & ~7) * S;  // workgroups of tokens 0 .. 8a-1
+  if (b < grouped) {
+    const int q = b >> 3;
+    const int tq = q / S;
+    t = (b & 7) + 8 * tq;
+    split = q - tq * S;
+  } else {
+    const int r = b - grouped;
+    const int tr = r / S;
+    t = (T & ~7) + tr;
+    split = r - tr * S;
+  }
+}
+
 constexpr int kWaveBlock = 16;                          // keys per block
 constexpr int kWaveWaves = 4;
 constexpr int kWaveKpeOff = kWaveBlock * kCkvPitch;     // 16640
@@ -1058,8 +1081,8 @@ __global__ __launch_bounds__(kWaveWaves * 64, 1) void dsa_attn_wave_kernel(AttnP
   __shared__ __attribute__((aligned(16))) char lds[kWaveLds];
   int32_t *slots = (int32_t *)(lds + kWaveWaves * kWaveRing);
 
-  const int t = blockIdx.x / p.num_splits;
-  const int split = blockIdx.x - t * p.num_splits;
+  int t, split;
+  xcd_token_split(p.T, p.num_splits, t, split);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r16 = lane & 15;
@@ -1356,36 +1379,43 @@ __global__ __launch_bounds__(kWaveWaves * 64, 1) void dsa_attn_wave_kernel(AttnP
     for (int f = 0; f < 8; ++f) sl[f * 64 + lane] = acc[dst * 8 + f];
   }
   lds_barrier();
-  float M = -INFINITY;
-  float mw[kWaveWaves], lw[kWaveWaves];
+  // Every read is issued before the first use (one LDS round trip): the four
+  // (m, l) pairs and the slices the other three waves wrote for this one.
+  float2 pr[kWaveWaves];
 #pragma unroll
-  for (int w = 0; w < kWaveWaves; ++w) {
-    const float2 v = pairs(w)[r16];
-    mw[w] = v.x;
-    lw[w] = v.y;
-    M = fmaxf(M, v.x);
+  for (int w = 0; w < kWaveWaves; ++w) pr[w] = pairs(w)[r16];
+  f32x4 oth[kWaveWaves - 1][8];
+#pragma unroll
+  for (int i = 0; i < kWaveWaves - 1; ++i) {
+    const f32x4 *sl = slice(i + (i >= wave), wave);
+#pragma unroll
+    for (int f = 0; f < 8; ++f) oth[i][f] = sl[f * 64 + lane];
   }
+  // M and L in wave order, so every wave of the workgroup gets the same bits
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kWaveWaves; ++w) M = fmaxf(M, pr[w].x);
   float L = 0.f, aw[kWaveWaves];
 #pragma unroll
   for (int w = 0; w < kWaveWaves; ++w) {
-    aw[w] = (mw[w] == -INFINITY) ? 0.f : fast_exp2(mw[w] - M);
-    L += aw[w] * lw[w];
+    aw[w] = (pr[w].x == -INFINITY) ? 0.f : fast_exp2(pr[w].x - M);
+    L += aw[w] * pr[w].y;
   }
-  // this wave's own blocks (static register indices: one uniform branch per wave)
-  f32x4 mine[8];
+  // this wave's own blocks first, then the other waves' in ascending order (a
+  // fixed order for each wave: deterministic sums); static register indices,
+  // one uniform branch per wave
+  f32x4 o[8];
 #pragma unroll
   for (int w = 0; w < kWaveWaves; ++w)
     if (w == wave) {
 #pragma unroll
-      for (int f = 0; f < 8; ++f) mine[f] = acc[w * 8 + f];
+      for (int f = 0; f < 8; ++f) o[f] = aw[w] * acc[w * 8 + f];
     }
-  f32x4 o[8];
 #pragma unroll
-  for (int f = 0; f < 8; ++f) o[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < kWaveWaves - 1; ++i) {
+    const float a = i < wave ? aw[i] : aw[i + 1];
 #pragma unroll
-  for (int w = 0; w < kWaveWaves; ++w) {  // wave order: deterministic sums
-#pragma unroll
-    for (int f = 0; f < 8; ++f) o[f] += aw[w] * ((w == wave) ? mine[f] : slice(w, wave)[f * 64 + lane]);
+    for (int f = 0; f < 8; ++f) o[f] += a * oth[i][f];
   }
 
   if (p.num_splits == 1 && !p.partial_only) {
