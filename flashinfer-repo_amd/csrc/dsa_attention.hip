@@ -490,7 +490,10 @@ __device__ __forceinline__ void split_partial(const AttnParams &p, int t, int sp
   uint32_t *cnt = p.counters + ((int64_t)t * gridDim.y + blockIdx.y) * 8 + wave;
   uint32_t ticket = 0;
   if (lane == 0) ticket = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  ticket = __shfl(ticket, 0);
+  // lane 0's ticket as a scalar: kept in a VGPR, the compiler substitutes it
+  // for S - 1 below and the buffer resources built from it become per-lane
+  // values, each load then wrapped in a waterfall loop
+  ticket = __builtin_amdgcn_readfirstlane(ticket);
   if (ticket != (uint32_t)(S - 1)) return;
   if (lane == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
