@@ -233,6 +233,38 @@ __device__ __forceinline__ void tr_wait_all(u32x2 (&prev)[8]) {
                : "memory");
 }
 
+// Q^T of one head group from its LDS staging (see the wave kernel): k-steps
+// 0..15 at qn + 64 k, k-steps 16, 17 at qp and qp + 64, with the wait, in one
+// asm statement (the compiler would wait for every LDS DMA in flight before
+// the builtin form).
+__device__ __forceinline__ void q_read18(uint32_t qn, uint32_t qp, bf16x8 (&q)[18]) {
+  asm volatile(
+      "ds_read_b128 %0, %18\n\t"
+      "ds_read_b128 %1, %18 offset:64\n\t"
+      "ds_read_b128 %2, %18 offset:128\n\t"
+      "ds_read_b128 %3, %18 offset:192\n\t"
+      "ds_read_b128 %4, %18 offset:256\n\t"
+      "ds_read_b128 %5, %18 offset:320\n\t"
+      "ds_read_b128 %6, %18 offset:384\n\t"
+      "ds_read_b128 %7, %18 offset:448\n\t"
+      "ds_read_b128 %8, %18 offset:512\n\t"
+      "ds_read_b128 %9, %18 offset:576\n\t"
+      "ds_read_b128 %10, %18 offset:640\n\t"
+      "ds_read_b128 %11, %18 offset:704\n\t"
+      "ds_read_b128 %12, %18 offset:768\n\t"
+      "ds_read_b128 %13, %18 offset:832\n\t"
+      "ds_read_b128 %14, %18 offset:896\n\t"
+      "ds_read_b128 %15, %18 offset:960\n\t"
+      "ds_read_b128 %16, %19\n\t"
+      "ds_read_b128 %17, %19 offset:64\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(q[0]), "=&v"(q[1]), "=&v"(q[2]), "=&v"(q[3]), "=&v"(q[4]), "=&v"(q[5]), "=&v"(q[6]),
+        "=&v"(q[7]), "=&v"(q[8]), "=&v"(q[9]), "=&v"(q[10]), "=&v"(q[11]), "=&v"(q[12]),
+        "=&v"(q[13]), "=&v"(q[14]), "=&v"(q[15]), "=&v"(q[16]), "=&v"(q[17])
+      : "v"(qn), "v"(qp)
+      : "memory");
+}
+
 // tr_read4 for every feature block of a wave's slice, four at a time, each
 // batch followed by its MFMAs (fn(f0, av)).
 template <int NFB, int ROWB, int F0 = 0, typename Fn>
@@ -1098,9 +1130,9 @@ __global__ __launch_bounds__(kWaveWaves * 64, 1) void dsa_attn_wave_kernel(AttnP
   const int my_blocks = n_blocks * (wave + 1) / kWaveWaves - b0;
   char *ring = lds + wave * kWaveRing;
 
-  // Prologue: this wave's ids are loaded first, then Q^T; the ids are sorted
-  // and the first gather issued while Q is still in flight (vector loads
-  // complete in issue order, so the loop's stage waits cover Q).
+  // Prologue: this wave's ids are loaded and sorted, its quarter of the
+  // workgroup's Q is staged in LDS, the first gather is issued, and Q^T is
+  // read into registers from the staging.
   constexpr int kPer = kWaveIds / (kWaveWaves * 64);  // ids per lane (a wave takes <= 512 keys)
   const int32_t *isrc = p.idx + (int64_t)t * p.idx_st + k_begin + b0 * kWaveBlock;
   const int n_mine = my_blocks * kWaveBlock;  // keys of this wave's blocks (tail padding included)
@@ -1110,17 +1142,6 @@ __global__ __launch_bounds__(kWaveWaves * 64, 1) void dsa_attn_wave_kernel(AttnP
   for (int k = 0; k < kPer; ++k) {
     const int i = k * 64 + lane;
     sv[k] = i < n_real ? isrc[i] : -1;
-  }
-  // Q^T as the B operand of S^T = K Q^T: k-step k < 16 holds q_nope features
-  // 32k + 8g .. +7 of head `head`, k-steps 16, 17 the q_pe features.
-  bf16x8 q[18];
-  {
-    const char *qn = p.q_nope + t * p.qn_st + head * p.qn_sh + g * 16;
-    const char *qp = p.q_pe + t * p.qp_st + head * p.qp_sh + g * 16;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) q[k] = *(const bf16x8 *)(qn + k * 64);
-#pragma unroll
-    for (int k = 0; k < 2; ++k) q[16 + k] = *(const bf16x8 *)(qp + k * 64);
   }
   auto valid_id = [&](int s) { return (s >= 0 && (int64_t)s < p.num_slots) ? s : -1; };
 
@@ -1199,6 +1220,29 @@ __global__ __launch_bounds__(kWaveWaves * 64, 1) void dsa_attn_wave_kernel(AttnP
 #pragma unroll
   for (int k = 0; k < kPer; ++k)
     if (bk[k] >= 0) my_ids[start[k * 256 + bk[k]] + rk[k]] = sv[k];
+  // ---- Q of the head group, staged once per workgroup (a quarter of the
+  // traffic of every wave loading all of it, and issued after the sort so
+  // the loads sorted ids wait for are not queued behind it): wave w DMAs the
+  // q_nope rows of heads 4w .. 4w+3 (pitch 1040 bytes: the 16 heads' reads
+  // of one k-step land on distinct banks) and their q_pe rows (pitch 128)
+  // into the second stage of wave 0's ring, which the loop first fills with
+  // wave 0's second block.
+  char *qstage = lds + kWaveStage;
+  constexpr int kQPePos = kHeadsPerGroup * kCkvPitch;  // q_pe rows after the 16 q_nope rows
+  static_assert(kQPePos + kHeadsPerGroup * 128 <= kWaveStage, "Q staging fits one stage");
+  {
+    const int hb = blockIdx.y * kHeadsPerGroup;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * wave + i;
+      lds_dma16(p.q_nope + t * p.qn_st + (hb + h) * p.qn_sh + lane * 16, qstage + h * kCkvPitch);
+    }
+    if (lane < 32) {
+      const int h = 4 * wave + (lane >> 3);
+      lds_dma16(p.q_pe + t * p.qp_st + (hb + h) * p.qp_sh + (lane & 7) * 16,
+                qstage + kQPePos + 4 * wave * 128);
+    }
+  }
   const int id0 = my_blocks > 0 ? my_ids[r16] : -1;
 
   const auto ckv_rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)p.ckv, 0, (int)p.ckv_extent, kBufferFlags);
@@ -1240,6 +1284,21 @@ __global__ __launch_bounds__(kWaveWaves * 64, 1) void dsa_attn_wave_kernel(AttnP
     return valid;
   };
   uint32_t vm_next = my_blocks > 0 ? gather(id0, 0) : 0u;
+  // Q^T, the B operand of S^T = K Q^T: k-step k < 16 holds q_nope features
+  // 32k + 8g .. +7 of head `head`, k-steps 16, 17 the q_pe features.  Every
+  // wave's staging DMAs (issued before its first gather) have landed after
+  // its wait and the barrier; the second barrier frees the staging for wave
+  // 0's second block.
+  if (my_blocks > 0)
+    wait_vmcnt<18>();
+  else
+    wait_vmcnt<0>();
+  __builtin_amdgcn_s_barrier();
+  bf16x8 q[18];
+  q_read18((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)(qstage + r16 * kCkvPitch + g * 16),
+           (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)(qstage + kQPePos + r16 * 128 + g * 16),
+           q);
+  __builtin_amdgcn_s_barrier();
 
   f32x4 acc[32];
 #pragma unroll
