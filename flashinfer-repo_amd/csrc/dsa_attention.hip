@@ -1076,29 +1076,6 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
 // 16 kpe rows chunk-major (16-byte chunk c of key k at 256 c + 16 k), so the
 // QK operand reads (16 rows, one column) and the transposing V^T reads (rows
 // key_of_row(4g + j)) are free of bank conflicts.
-// (token, chunk) of this workgroup.  Workgroups are dispatched to the eight
-// XCDs round robin (linear workgroup id mod 8), so the chunks of a token are
-// given ids of one residue mod 8: they share an XCD and its L2 (the token's Q
-// is fetched into one L2 instead of S, and the split exchange stays on one
-// XCD).  Tokens 8a .. T-1 (T = 8a + r) keep the plain order after them.  The
-// merge does not depend on this placement (its accesses are device
-// coherent); only the speed does.
-__device__ __forceinline__ void xcd_token_split(int T, int S, int &t, int &split) {
-  const int b = blockIdx.x;
-  const int grouped = (T & ~7) * S;  // workgroups of tokens 0 .. 8a-1
-  if (b < grouped) {
-    const int q = b >> 3;
-    const int tq = q / S;
-    t = (b & 7) + 8 * tq;
-    split = q - tq * S;
-  } else {
-    const int r = b - grouped;
-    const int tr = r / S;
-    t = (T & ~7) + tr;
-    split = r - tr * S;
-  }
-}
-
 constexpr int kWaveBlock = 16;                          // keys per block
 constexpr int kWaveWaves = 4;
 constexpr int kWaveKpeOff = kWaveBlock * kCkvPitch;     // 16640
@@ -1116,8 +1093,8 @@ __global__ __launch_bounds__(kWaveWaves * 64, 1) void dsa_attn_wave_kernel(AttnP
   __shared__ __attribute__((aligned(16))) char lds[kWaveLds];
   int32_t *slots = (int32_t *)(lds + kWaveWaves * kWaveRing);
 
-  int t, split;
-  xcd_token_split(p.T, p.num_splits, t, split);
+  const int t = blockIdx.x / p.num_splits;
+  const int split = blockIdx.x - t * p.num_splits;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r16 = lane & 15;
