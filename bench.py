@@ -339,9 +339,11 @@ def measure_attention(name, d, steps, warmup, cold_copies=0):
             "traffic": hbm["traffic"], "algorithmic_flops": alg_flops, "kernel": kdesc,
             "counters": hbm["counters"]}
     # Config 3 is the MFMA-bound shape by the target's definition (its gathers
-    # hit a 40 MB causal window the caches hold); the others are priced
-    # against HBM, with the MFMA fraction beside it.
-    roofline, other = (mfma, hbm) if name == "cfg3" else (hbm, mfma)
+    # hit a 40 MB causal window the caches hold), and config 4 is the dense
+    # contraction with 128 heads on the MFMA M dimension (its counters show the
+    # MFMA pipe, not HBM, as the busy unit); the others are priced against
+    # HBM, with the MFMA fraction beside it.
+    roofline, other = (mfma, hbm) if name in ("cfg3", "cfg4") else (hbm, mfma)
     cache_slots = d["ckv_cache"].numel() // 512
     ps = d["ckv_cache"].shape[1] if d["ckv_cache"].dim() == 3 else 1
     return {
