@@ -916,8 +916,10 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
     // QK/PV of a tile runs while the other team does its softmax.  Before a
     // barrier that lets either team compute tile j, both teams' shares of
     // tile j have landed: A waits before X_j, B before Y_{j-1}.  The stage of
-    // tile j-2 is free once both teams passed their fused step j-1: at the
-    // pair (A's X_j, B's Y_{j-1}), where both fire their shares of tile j+2.
+    // tile j-2 is free once both teams passed their fused step j-1, i.e.
+    // after the pair (A's X_j, B's Y_{j-1}): B fires its share of tile j+2
+    // right after that pair (before its softmax of tile j-1), A after its
+    // softmax of tile j (while B runs its fused step j).
     int fired = pre - 1;  // last tile whose share this wave has issued
     auto wait_own = [&](int j) {  // this wave's share of tile j landed
       const int ahead = fired - j;
@@ -938,10 +940,6 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
     for (int j = 0; j < n_tiles; ++j) {
       wait_own(j);
       __builtin_amdgcn_s_barrier();  // X_j
-      if (!team_b && j + 2 < n_tiles) {
-        fire_tile(j + 2, tile_src(j + 2));
-        fired = j + 2;
-      }
       fused(j, sb);
       if (team_b && j + 1 < n_tiles) wait_own(j + 1);
       __builtin_amdgcn_s_waitcnt(0xC07F);
@@ -951,6 +949,12 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
         fired = j + 3;
       }
       softmax(sb, __builtin_amdgcn_readlane(tile_masks, j), p_hi, p_lo);
+      // team A issues its share of tile j+2 here, where it waits for team B's
+      // QK/PV anyway, not between X_j and its own QK/PV
+      if (!team_b && j + 2 < n_tiles) {
+        fire_tile(j + 2, tile_src(j + 2));
+        fired = j + 2;
+      }
     }
     if (!team_b) __builtin_amdgcn_s_barrier();
   } else {
