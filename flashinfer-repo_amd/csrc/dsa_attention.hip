@@ -1202,8 +1202,8 @@ __global__ __launch_bounds__(kWaveWaves * 64, 1) void dsa_attn_wave_kernel(AttnP
   for (int k = 0; k < kPer; ++k)
     if (bk[k] >= 0) my_ids[start[k * 256 + bk[k]] + rk[k]] = sv[k];
   // ---- Q of the head group, staged once per workgroup (a quarter of the
-  // traffic of every wave loading all of it, and issued after the sort so
-  // the loads sorted ids wait for are not queued behind it): wave w DMAs the
+  // traffic of every wave loading all of it, and issued after the sort, so
+  // the id loads the sort waits for are not queued behind it): wave w DMAs the
   // q_nope rows of heads 4w .. 4w+3 (pitch 1040 bytes: the 16 heads' reads
   // of one k-step land on distinct banks) and their q_pe rows (pitch 128)
   // into the second stage of wave 0's ring, which the loop first fills with
