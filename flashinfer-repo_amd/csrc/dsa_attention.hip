@@ -292,6 +292,14 @@ __device__ __forceinline__ uint64_t readlane64(uint64_t v, int lane) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// o += a * x with one rounding per component, written out: the split merges
+// must give the same bits in every kernel, and an add that the compiler
+// moves past a branch is no longer contracted with its product.
+__device__ __forceinline__ void fma_to(f32x4 &o, float a, const f32x4 &x) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) o[k] = __builtin_fmaf(a, x[k], o[k]);
+}
+
 // Key (within a 16-key block) that MFMA row m of S^T stands for.
 __device__ __forceinline__ int key_of_row(int m) {
   return ((m >> 2) & 1) * 8 + (m >> 3) + 2 * (m & 3);
@@ -573,13 +581,13 @@ __device__ __forceinline__ void split_partial(const AttnParams &p, int t, int sp
 #pragma unroll
       for (int j = 0; j < kB; ++j) {
         a[j] = (ml[j].x == -INFINITY) ? 0.f : fast_exp2(ml[j].x - M);
-        if (fc == 0 && s0 + j < S) L += a[j] * ml[j].y;
+        if (fc == 0 && s0 + j < S) L = __builtin_fmaf(a[j], ml[j].y, L);
       }
 #pragma unroll
       for (int j = 0; j < kB; ++j)
         if (s0 + j < S) {
 #pragma unroll
-          for (int f = 0; f < kF; ++f) o[f] += a[j] * pa[j][f];
+          for (int f = 0; f < kF; ++f) fma_to(o[f], a[j], pa[j][f]);
         }
     }
     if (fc == 0) inv = (M == -INFINITY) ? 0.f : 1.f / L;
@@ -1086,6 +1094,7 @@ constexpr int kWaveKpeOff = kWaveBlock * kCkvPitch;     // 16640
 constexpr int kWaveStage = kWaveKpeOff + kWaveBlock * 128;  // + 2048 = 18688
 constexpr int kWaveRing = 2 * kWaveStage;
 constexpr int kWaveIds = kMaxChunkWide;                 // slot ids of a chunk, staged once
+constexpr int kWaveSortBlocks = 16;  // a wave sorts its keys by slot from this many blocks on
 constexpr int kWaveLds = kWaveWaves * kWaveRing + kWaveIds * 4;
 static_assert(kWaveLds <= 160 * 1024, "LDS budget of one gfx950 CU");
 // the merge after the loop reuses each wave's ring: three 8 KB slices (one
@@ -1126,81 +1135,89 @@ __global__ __launch_bounds__(kWaveWaves * 64, 1) void dsa_attn_wave_kernel(AttnP
   }
   auto valid_id = [&](int s) { return (s >= 0 && (int64_t)s < p.num_slots) ? s : -1; };
 
-  // ---- order this wave's keys by slot: a stable counting sort on the top 8
-  // bits of the slot id (256 buckets, each a contiguous range of the cache),
-  // in the wave's own (not yet used) ring, so no workgroup barrier is
-  // needed: one wave's LDS accesses execute in program order.  Every wave of
-  // every workgroup then sweeps the cache upwards at the same time, which
-  // keeps address translation and cache lines shared between neighbouring
-  // gathers.  The order depends on the ids alone: results stay
-  // deterministic.  Scratch: per-vector bucket counts hist[k][256] (bytes;
-  // vector k = keys 64k .. 64k+63 of the wave), their start positions
-  // start[k][256] (u16); the sorted ids go to the wave's 512-entry slice of
-  // the id array.
-  uint8_t *hist = (uint8_t *)ring;
-  uint16_t *start = (uint16_t *)(ring + kPer * 256);
   int32_t *my_ids = slots + wave * (kWaveIds / kWaveWaves);
-  static_assert(kPer * 256 * 3 <= kWaveRing, "sort scratch in the ring");
-  *(u32x4 *)(hist + lane * 32) = u32x4{0u, 0u, 0u, 0u};
-  *(u32x4 *)(hist + lane * 32 + 16) = u32x4{0u, 0u, 0u, 0u};
-  const uint32_t top = (uint32_t)min(p.num_slots, (int64_t)0x7fffffff);
-  const int shift = max(0, (32 - __builtin_clz(max(top, 1u))) - 8);
-  int bk[kPer], rk[kPer];
+  if (my_blocks < kWaveSortBlocks) {
+    // few blocks: the keys keep their given order (the sort below costs
+    // about 1 us of the prologue and pays only on long runs)
 #pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const int id = valid_id(sv[k]);
-    sv[k] = id;
-    const int b = k * 64 + lane < n_mine ? (id >= 0 ? (id >> shift) : 255) : -1;
-    bk[k] = b;
-    rk[k] = 0;
-    if (k * 64 < n_mine) {  // wave-uniform
-      uint64_t same = __ballot(b >= 0);
-#pragma unroll
-      for (int bit = 0; bit < 8; ++bit) {
-        const bool on = (b >> bit) & 1;
-        const uint64_t bb = __ballot(on);
-        same &= on ? bb : ~bb;
-      }
-      const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(same >> 32),
-                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)same, 0));
-      rk[k] = rank;
-      if (b >= 0 && rank == __popcll(same) - 1) hist[k * 256 + b] = (uint8_t)(rank + 1);
-    }
-  }
-  {
-    // lane l owns buckets 4l .. 4l+3
-    uint32_t pre[kPer][4], tot[4] = {0u, 0u, 0u, 0u};
+    for (int k = 0; k < kPer; ++k)
+      if (k * 64 + lane < n_mine) my_ids[k * 64 + lane] = valid_id(sv[k]);
+  } else {
+    // ---- order this wave's keys by slot: a stable counting sort on the top 8
+    // bits of the slot id (256 buckets, each a contiguous range of the cache),
+    // in the wave's own (not yet used) ring, so no workgroup barrier is
+    // needed: one wave's LDS accesses execute in program order.  Every wave of
+    // every workgroup then sweeps the cache upwards at the same time, which
+    // keeps address translation and cache lines shared between neighbouring
+    // gathers.  The order depends on the ids alone: results stay
+    // deterministic.  Scratch: per-vector bucket counts hist[k][256] (bytes;
+    // vector k = keys 64k .. 64k+63 of the wave), their start positions
+    // start[k][256] (u16); the sorted ids go to the wave's 512-entry slice of
+    // the id array.
+    uint8_t *hist = (uint8_t *)ring;
+    uint16_t *start = (uint16_t *)(ring + kPer * 256);
+    static_assert(kPer * 256 * 3 <= kWaveRing, "sort scratch in the ring");
+    *(u32x4 *)(hist + lane * 32) = u32x4{0u, 0u, 0u, 0u};
+    *(u32x4 *)(hist + lane * 32 + 16) = u32x4{0u, 0u, 0u, 0u};
+    const uint32_t top = (uint32_t)min(p.num_slots, (int64_t)0x7fffffff);
+    const int shift = max(0, (32 - __builtin_clz(max(top, 1u))) - 8);
+    int bk[kPer], rk[kPer];
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
-      const uint32_t c4 = *(const uint32_t *)(hist + k * 256 + lane * 4);
+      const int id = valid_id(sv[k]);
+      sv[k] = id;
+      const int b = k * 64 + lane < n_mine ? (id >= 0 ? (id >> shift) : 255) : -1;
+      bk[k] = b;
+      rk[k] = 0;
+      if (k * 64 < n_mine) {  // wave-uniform
+        uint64_t same = __ballot(b >= 0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        pre[k][i] = tot[i];
-        tot[i] += (c4 >> (8 * i)) & 255u;
+        for (int bit = 0; bit < 8; ++bit) {
+          const bool on = (b >> bit) & 1;
+          const uint64_t bb = __ballot(on);
+          same &= on ? bb : ~bb;
+        }
+        const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(same >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)same, 0));
+        rk[k] = rank;
+        if (b >= 0 && rank == __popcll(same) - 1) hist[k * 256 + b] = (uint8_t)(rank + 1);
       }
     }
-    const int lsum = (int)(tot[0] + tot[1] + tot[2] + tot[3]);
-    int incl = lsum;
-    incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xf, 0xf, false);  // row_shr:1
-    incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xf, 0xf, false);  // row_shr:2
-    incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xf, 0xf, false);  // row_shr:4
-    incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xf, 0xf, false);  // row_shr:8
-    incl += __builtin_amdgcn_update_dpp(0, incl, 0x142, 0xa, 0xf, false);  // row_bcast:15
-    incl += __builtin_amdgcn_update_dpp(0, incl, 0x143, 0xc, 0xf, false);  // row_bcast:31
-    uint32_t base[4];
-    base[0] = (uint32_t)(incl - lsum);
+    {
+      // lane l owns buckets 4l .. 4l+3
+      uint32_t pre[kPer][4], tot[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int i = 1; i < 4; ++i) base[i] = base[i - 1] + tot[i - 1];
+      for (int k = 0; k < kPer; ++k) {
+        const uint32_t c4 = *(const uint32_t *)(hist + k * 256 + lane * 4);
 #pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const uint32_t lo = (base[0] + pre[k][0]) | ((base[1] + pre[k][1]) << 16);
-      const uint32_t hi = (base[2] + pre[k][2]) | ((base[3] + pre[k][3]) << 16);
-      *(u32x2 *)(start + k * 256 + lane * 4) = u32x2{lo, hi};
+        for (int i = 0; i < 4; ++i) {
+          pre[k][i] = tot[i];
+          tot[i] += (c4 >> (8 * i)) & 255u;
+        }
+      }
+      const int lsum = (int)(tot[0] + tot[1] + tot[2] + tot[3]);
+      int incl = lsum;
+      incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xf, 0xf, false);  // row_shr:1
+      incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xf, 0xf, false);  // row_shr:2
+      incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xf, 0xf, false);  // row_shr:4
+      incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xf, 0xf, false);  // row_shr:8
+      incl += __builtin_amdgcn_update_dpp(0, incl, 0x142, 0xa, 0xf, false);  // row_bcast:15
+      incl += __builtin_amdgcn_update_dpp(0, incl, 0x143, 0xc, 0xf, false);  // row_bcast:31
+      uint32_t base[4];
+      base[0] = (uint32_t)(incl - lsum);
+#pragma unroll
+      for (int i = 1; i < 4; ++i) base[i] = base[i - 1] + tot[i - 1];
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) {
+        const uint32_t lo = (base[0] + pre[k][0]) | ((base[1] + pre[k][1]) << 16);
+        const uint32_t hi = (base[2] + pre[k][2]) | ((base[3] + pre[k][3]) << 16);
+        *(u32x2 *)(start + k * 256 + lane * 4) = u32x2{lo, hi};
+      }
     }
-  }
 #pragma unroll
-  for (int k = 0; k < kPer; ++k)
-    if (bk[k] >= 0) my_ids[start[k * 256 + bk[k]] + rk[k]] = sv[k];
+    for (int k = 0; k < kPer; ++k)
+      if (bk[k] >= 0) my_ids[start[k * 256 + bk[k]] + rk[k]] = sv[k];
+  }
   // ---- Q of the head group, staged once per workgroup (a quarter of the
   // traffic of every wave loading all of it, and issued after the sort, so
   // the id loads the sort waits for are not queued behind it): wave w DMAs the
@@ -1511,8 +1528,8 @@ __global__ __launch_bounds__(128) void dsa_attn_combine_kernel(AttnParams p) {
     for (int s = 0; s < SMAX; ++s) {
       if (s < S) {
         const float a = (ml[s].x == -INFINITY) ? 0.f : fast_exp2(ml[s].x - M);
-        L += a * ml[s].y;
-        o += a * pa[s];
+        L = __builtin_fmaf(a, ml[s].y, L);
+        fma_to(o, a, pa[s]);
       }
     }
   } else {
@@ -1521,8 +1538,8 @@ __global__ __launch_bounds__(128) void dsa_attn_combine_kernel(AttnParams p) {
       const int64_t row = row0 + (int64_t)s * p.H;
       const float ms = p.part_ml[row * 2];
       const float a = (ms == -INFINITY) ? 0.f : fast_exp2(ms - M);
-      L += a * p.part_ml[row * 2 + 1];
-      o += a * *(const f32x4 *)(p.part_acc + row * kHeadDimCkv + f0);
+      L = __builtin_fmaf(a, p.part_ml[row * 2 + 1], L);
+      fma_to(o, a, *(const f32x4 *)(p.part_acc + row * kHeadDimCkv + f0));
     }
   }
   const float inv = (M == -INFINITY) ? 0.f : 1.f / L;
