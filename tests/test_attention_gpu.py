@@ -439,6 +439,35 @@ def test_head_counts_match_oracle(H):
     _assert_parity(out, lse, *_oracle(d), f"H={H}")
 
 
+@pytest.mark.parametrize("K", [992, 1000])
+def test_sorted_and_unsorted_waves_in_one_workgroup(K):
+    """A wave orders its keys by slot only from 16 blocks on.  One chunk of
+    62 blocks (K = 992) gives the four waves 15, 16, 15 and 16 blocks, and 63
+    blocks (K = 1000, the last one ragged) 15, 16, 16 and 16: waves that sort
+    and waves that keep the given order share a workgroup and its merge.
+    Against the oracle (padding in one row, an out-of-range id in another),
+    bitwise against kernel_partial + merge_partials, and repeatable."""
+    d = workloads.cfg2(T=3, seed=700 + K)
+    idx = d["sparse_indices"][:, :K].clone()
+    idx[1, K - 40:] = -1
+    idx[2, 17] = 1 << 30
+    d["sparse_indices"] = idx
+    print(f"sorted and unsorted waves K={K}", flush=True)
+    out, lse = _run(kernel_splitk, d, SPLIT_K=1)
+    clean = idx.clone()
+    clean[(clean < 0) | (clean >= 131072)] = -1
+    _assert_parity(out, lse, *_oracle(dict(d, sparse_indices=clean)), f"K={K}")
+    g = workloads.to_device(d, DEV)
+    args = (g["q_nope"], g["q_pe"], g["ckv_cache"], g["kpe_cache"], g["sparse_indices"],
+            d["sm_scale"])
+    acc, ml = kernel_partial(*args, num_splits=1)
+    p_out, p_lse = merge_partials(acc, ml)
+    out2, lse2 = kernel_splitk(*args, SPLIT_K=1)
+    torch.cuda.synchronize()
+    assert torch.equal(out2.cpu(), out) and torch.equal(lse2.cpu(), lse)
+    assert torch.equal(p_out.cpu(), out) and torch.equal(p_lse.cpu(), lse)
+
+
 def test_in_kernel_merge_counters_reused_across_calls_and_shapes():
     """One counter buffer serves consecutive calls of different shapes and
     split counts; each result equals the merge-kernel path."""
