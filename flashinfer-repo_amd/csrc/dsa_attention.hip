@@ -1066,9 +1066,9 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
 // Layout for head counts of an odd number of 16-head groups (H = 16 decode
 // and prefill): one workgroup per (token, top-k chunk, head group) with four
 // waves, one per SIMD.  Each wave owns a quarter of the chunk's 16-key blocks
-// (its keys taken in ascending slot order) and runs on its own: its blocks
-// are gathered by LDS DMA into a private
-// two-stage ring (block j+1 in flight while block j is computed), its scores
+// (from 16 blocks on its keys taken in ascending slot order) and runs on its
+// own: its blocks are gathered by LDS DMA into a private two-stage ring
+// (block j+1 in flight while block j is computed), its scores
 // are complete (the whole 576-wide QK per wave: no partial-score exchange),
 // and its online softmax and O^T accumulator cover its own keys only.  No
 // workgroup barrier sits in the loop, so a wave waiting for a slow gather
@@ -1120,9 +1120,9 @@ __global__ __launch_bounds__(kWaveWaves * 64, 1) void dsa_attn_wave_kernel(AttnP
   const int my_blocks = n_blocks * (wave + 1) / kWaveWaves - b0;
   char *ring = lds + wave * kWaveRing;
 
-  // Prologue: this wave's ids are loaded and sorted, its quarter of the
-  // workgroup's Q is staged in LDS, the first gather is issued, and Q^T is
-  // read into registers from the staging.
+  // Prologue: this wave's ids are loaded (and, on long runs, sorted), its
+  // quarter of the workgroup's Q is staged in LDS, the first gather is
+  // issued, and Q^T is read into registers from the staging.
   constexpr int kPer = kWaveIds / (kWaveWaves * 64);  // ids per lane (a wave takes <= 512 keys)
   const int32_t *isrc = p.idx + (int64_t)t * p.idx_st + k_begin + b0 * kWaveBlock;
   const int n_mine = my_blocks * kWaveBlock;  // keys of this wave's blocks (tail padding included)
@@ -1219,8 +1219,9 @@ __global__ __launch_bounds__(kWaveWaves * 64, 1) void dsa_attn_wave_kernel(AttnP
       if (bk[k] >= 0) my_ids[start[k * 256 + bk[k]] + rk[k]] = sv[k];
   }
   // ---- Q of the head group, staged once per workgroup (a quarter of the
-  // traffic of every wave loading all of it, and issued after the sort, so
-  // the id loads the sort waits for are not queued behind it): wave w DMAs the
+  // traffic of every wave loading all of it, and issued after the ids are
+  // stored, so the id loads that store waits for are not queued behind it;
+  // issued right after the id loads instead it gained nothing): wave w DMAs the
   // q_nope rows of heads 4w .. 4w+3 (pitch 1040 bytes: the 16 heads' reads
   // of one k-step land on distinct banks) and their q_pe rows (pitch 128)
   // into the second stage of wave 0's ring, which the loop first fills with
