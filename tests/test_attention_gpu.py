@@ -468,6 +468,39 @@ def test_sorted_and_unsorted_waves_in_one_workgroup(K):
     assert torch.equal(p_out.cpu(), out) and torch.equal(p_lse.cpu(), lse)
 
 
+@pytest.mark.parametrize("case", range(12))
+def test_random_shapes_match_oracle(case):
+    """Seeded random shapes across every kernel layout (H = 16 .. 128 in
+    16-head groups, odd and even group counts), page sizes 1, 16, 64 and
+    100, top-k from 1 to 3000 with padding, empty rows and out-of-range ids,
+    automatic and explicit split counts."""
+    rng = np.random.default_rng(4000 + case)
+    T = int(rng.integers(1, 24))
+    H = int(rng.choice([16, 32, 48, 64, 80, 128]))
+    ps = int(rng.choice([1, 16, 64, 100]))
+    pages = int(rng.integers(8, 64)) * max(1, 64 // ps)
+    slots = pages * ps
+    K = int(rng.integers(1, min(3000, slots) + 1))
+    d = workloads.attention_inputs(T, H, K, pages, ps, seed=5000 + case)
+    g = d.pop("gen")
+    idx = torch.stack([torch.randperm(slots, generator=g)[:K] for _ in range(T)]).to(torch.int32)
+    idx[torch.rand(idx.shape, generator=g) < float(rng.choice([0.0, 0.1, 0.6]))] = -1
+    if T > 1 and rng.random() < 0.3:
+        idx[0] = -1
+    if rng.random() < 0.3:
+        idx[-1, :min(K, 40)] = slots + 5
+    clean = idx.clone()
+    clean[(clean < 0) | (clean >= slots)] = -1
+    d.update(sparse_indices=idx, sm_scale=float(rng.uniform(0.03, 0.12)))
+    splits = int(rng.choice([0, 1, 3, 7, 16]))
+    print(f"random case {case}: T={T} H={H} page={ps} slots={slots} K={K} splits={splits}", flush=True)
+    if splits == 0:
+        out, lse = _run(kernel, d)
+    else:
+        out, lse = _run(kernel_splitk, d, SPLIT_K=splits)
+    _assert_parity(out, lse, *_oracle(dict(d, sparse_indices=clean)), f"random case {case}")
+
+
 def test_in_kernel_merge_counters_reused_across_calls_and_shapes():
     """One counter buffer serves consecutive calls of different shapes and
     split counts; each result equals the merge-kernel path."""
