@@ -1592,7 +1592,17 @@ hipError_t launch_attention_partial(const AttnParams &p, hipStream_t stream) {
   if (p.T == 0) return hipSuccess;
   const int groups = p.H / kHeadsPerGroup;
   const int hb = attn_head_blocks(p.H);
-  if (groups % 8 == 0) return launch_ring<8, 1>(p, hb, stream);  // one wave per head group
+  if (groups % 8 == 0) {
+    // Few workgroups (small-T decode): four-wave workgroups of four head
+    // groups each -- twice the workgroups, each gathering the chunk's keys --
+    // finish sooner while that grid still fits the CUs in one round (H=128,
+    // top-k 2048: T=1 28.0 -> 21.4 us, T=8 34.2 -> 27.8 us; the same bits);
+    // past that the eight-wave workgroups' shared gathers win (T=16 42.4
+    // against 53.1 us).
+    if ((int64_t)p.T * p.num_splits * (groups / 4) <= kNumCU)
+      return launch_ring<4, 1>(p, groups / 4, stream);
+    return launch_ring<8, 1>(p, hb, stream);  // one wave per head group
+  }
   if (groups % 4 == 0) return launch_ring<4, 1>(p, hb, stream);
   if (groups % 2 == 0) return launch_ring<8, 4>(p, hb, stream);  // 2 groups x 4 slices
   return launch_wave(p, hb, stream);                             // 1 group, 4 independent waves

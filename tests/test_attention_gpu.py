@@ -468,6 +468,26 @@ def test_sorted_and_unsorted_waves_in_one_workgroup(K):
     assert torch.equal(p_out.cpu(), out) and torch.equal(p_lse.cpu(), lse)
 
 
+def test_h128_small_grid_layout_same_bits():
+    """H = 128 calls whose grid is small (here T=8 with 4 chunks) run four-wave
+    workgroups of 64 heads; larger ones (T=40) eight-wave workgroups of 128
+    heads.  The eight tokens give the same bits either way (same chunks, the
+    same arithmetic per head group), and match the oracle."""
+    T, H, K = 40, 128, 700
+    d = workloads.attention_inputs(T, H, K, 64, 64, seed=4242)
+    g = d.pop("gen")
+    idx = torch.stack([torch.randperm(64 * 64, generator=g)[:K] for _ in range(T)]).to(torch.int32)
+    idx[3, 600:] = -1
+    d.update(sparse_indices=idx, sm_scale=0.0721)
+    print("H=128 layouts: T=8 and T=40, 4 chunks", flush=True)
+    out_all, lse_all = _run(kernel_splitk, d, SPLIT_K=4)
+    small = dict(d, q_nope=d["q_nope"][:8].clone(), q_pe=d["q_pe"][:8].clone(),
+                 sparse_indices=idx[:8].clone())
+    out8, lse8 = _run(kernel_splitk, small, SPLIT_K=4)
+    assert torch.equal(out8, out_all[:8]) and torch.equal(lse8, lse_all[:8])
+    _assert_parity(out8, lse8, *_oracle(small), "H=128 T=8")
+
+
 @pytest.mark.parametrize("case", range(12))
 def test_random_shapes_match_oracle(case):
     """Seeded random shapes across every kernel layout (H = 16 .. 128 in
