@@ -939,6 +939,8 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
         wait_vmcnt<0>();
     };
     if (team_b) {
+      // this barrier is team A's X_0: team B's share of tile 0 lands first
+      wait_own(0);
       __builtin_amdgcn_s_barrier();
       if (2 < n_tiles) {
         fire_tile(2, tile_src(2));

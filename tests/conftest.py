@@ -44,3 +44,14 @@ def mismatches(actual, expected, atol, rtol):
 def oracle_mod():
     import oracle
     return oracle
+
+
+def fill_lds_with_nan(device):
+    """Leaves NaN bit patterns in the LDS of every CU: a bf16 GEMM of NaN
+    operands (4096^3, more than one workgroup per CU) stages its tiles there,
+    and LDS is not cleared between workgroups.  A kernel launched next on the
+    same stream that reads an LDS location before writing it then computes
+    with NaN, which the parity checks see."""
+    import torch
+    a = torch.full((4096, 4096), float("nan"), dtype=torch.bfloat16, device=device)
+    return a @ a

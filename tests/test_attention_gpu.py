@@ -16,7 +16,7 @@ import pytest
 import torch
 
 import oracle
-from conftest import LSE_ATOL, LSE_RTOL, OUT_ATOL, OUT_RTOL, mismatches
+from conftest import LSE_ATOL, LSE_RTOL, OUT_ATOL, OUT_RTOL, fill_lds_with_nan, mismatches
 from dsa_amd import (kernel, kernel_out, kernel_partial, kernel_splitk, kernel_splitk_v2,
                      merge_partials, new_split_counters, new_workspace, workloads)
 
@@ -519,6 +519,34 @@ def test_random_shapes_match_oracle(case):
     else:
         out, lse = _run(kernel_splitk, d, SPLIT_K=splits)
     _assert_parity(out, lse, *_oracle(dict(d, sparse_indices=clean)), f"random case {case}")
+
+
+@pytest.mark.parametrize("H,T", [(16, 4), (48, 2), (32, 4), (64, 4), (128, 4), (128, 16), (128, 64)])
+def test_every_layout_after_nan_filled_lds(H, T):
+    """Each kernel layout (four independent waves; 2 groups x 4 slices; one
+    wave per group in four-wave workgroups, small and large H=128 grids; the
+    two-team eight-wave layout at T=16 with 16 chunks and at T=64) runs right
+    after a kernel that left NaN in every CU's LDS.  Every LDS location a
+    workgroup reads must have been written by its own gathers or stores
+    before the read: a stage read before all waves' gathers of it landed
+    turns the output NaN.  Several calls per shape, each on freshly
+    poisoned LDS."""
+    K = 2048
+    d = workloads.attention_inputs(T, H, K, 64, 64, seed=7100 + H + T)
+    g = d.pop("gen")
+    idx = torch.stack([torch.randperm(64 * 64, generator=g)[:K] for _ in range(T)]).to(torch.int32)
+    idx[0, 1900:] = -1
+    d.update(sparse_indices=idx, sm_scale=0.0721)
+    ref = _oracle(d)
+    gd = workloads.to_device({k: d[k] for k in ("q_nope", "q_pe", "ckv_cache", "kpe_cache",
+                                                "sparse_indices")}, DEV)
+    for r in range(6):
+        print(f"NaN-filled LDS H={H} T={T} call {r}", flush=True)
+        fill_lds_with_nan(DEV)
+        out, lse = kernel(gd["q_nope"], gd["q_pe"], gd["ckv_cache"], gd["kpe_cache"],
+                          gd["sparse_indices"], d["sm_scale"])
+        torch.cuda.synchronize()
+        _assert_parity(out.cpu(), lse.cpu(), *ref, f"H={H} T={T} call {r}")
 
 
 def test_in_kernel_merge_counters_reused_across_calls_and_shapes():

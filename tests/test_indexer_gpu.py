@@ -14,7 +14,7 @@ import pytest
 import torch
 
 import oracle
-from conftest import LSE_ATOL, LSE_RTOL, OUT_ATOL, OUT_RTOL, mismatches
+from conftest import LSE_ATOL, LSE_RTOL, OUT_ATOL, OUT_RTOL, fill_lds_with_nan, mismatches
 from dsa_amd import workloads
 from dsa_amd.indexer_kernel import run_indexer_and_topk, run_sparse_attention_pipeline
 
@@ -29,9 +29,11 @@ def _np(d):
             for k, v in d.items()}
 
 
-def _gpu_indexer(d, topk, block_table=None, page_size=64):
+def _gpu_indexer(d, topk, block_table=None, page_size=64, nan_lds=False):
     g = workloads.to_device(d, DEV)
     bt = None if block_table is None else block_table.to(DEV)
+    if nan_lds:
+        fill_lds_with_nan(DEV)
     out, scores = run_indexer_and_topk(g["q_idx"], g["k_idx"], g["k_scale"], g["weights"],
                                        g["causal_limit"], topk, block_table=bt,
                                        page_size=page_size, return_scores=True)
@@ -217,6 +219,21 @@ def test_cfg5_pipeline_end_to_end():
                                         NTHREADS)
     assert mismatches(out.float().cpu().numpy(), oracle.bf16_bits_to_f32(ref_out), OUT_ATOL, OUT_RTOL) == 0
     assert mismatches(lse.cpu().numpy(), ref_lse, LSE_ATOL, LSE_RTOL) == 0
+
+
+@pytest.mark.parametrize("T,Hi,S,topk", [(8, 64, 5000, 2048), (33, 48, 513, 17), (2, 16, 50000, 700),
+                                         (2, 16, 70000, 700), (3, 64, 9000, 300)])
+def test_after_nan_filled_lds(T, Hi, S, topk):
+    """Scores and selections (register top-k of 16 and 64 keys per thread,
+    the streaming top-k, rows shorter than top-k) right after a kernel that
+    left NaN in every CU's LDS: every LDS location the indexer kernels read
+    was written by them first, or the scores and sets would differ."""
+    d = workloads.indexer_inputs(T=T, Hi=Hi, S=S, seed=9100 + S)
+    ref_idx, ref_sc = _oracle(d, topk)
+    for r in range(3):
+        print(f"NaN-filled LDS indexer T={T} Hi={Hi} S={S} topk={topk} call {r}", flush=True)
+        got_idx, got_sc = _gpu_indexer(d, topk, nan_lds=True)
+        _assert_same(got_idx, got_sc, ref_idx, ref_sc, f"T={T} S={S} call {r}")
 
 
 @pytest.mark.parametrize("S", [12000, 50000, 70000])
