@@ -37,14 +37,23 @@ bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 constexpr int64_t kMaxWaveSplits = 8;
+constexpr int64_t kMaxEvenWaveSplits = 16;
 
 // Top-k chunk length per split and the split count that results.  Automatic
 // mode aims for about one workgroup per compute unit while keeping enough
 // work per chunk: four 32-key tiles for the shared-ring layouts; for the
-// four-wave layout (an odd number of 16-head groups) one 16-key block per
+// four-wave layout with an odd number of 16-head groups one 16-key block per
 // wave, and at most kMaxWaveSplits splits (measured at H=16, top-k 2048:
 // with 8 splits T = 1..16 run 1-3 us faster than with 16, whose longer
-// merge outweighs their parallelism; at T = 64, 4 splits).  An explicit
+// in-kernel merge outweighs their parallelism; at T = 64, 4 splits).  An
+// even number of groups takes the four-wave layout while T x groups <= 128,
+// with the most splits that keep its T x S x groups workgroups within one
+// round (chunks of at least 128 keys, at most kMaxEvenWaveSplits: 16 beat 8
+// by 1-2 us at T = 1..4 there, the separate merge kernel being cheap);
+// past that the shared-ring layouts, with the split count that fills one
+// round of their workgroups (H=128, top-k 2048, measured over T = 1..64 and
+// every layout and split count: the fastest configuration of each shape was
+// within 1.5 us of a grid of about one workgroup per CU).  An explicit
 // request is honoured up to one key per split (the reference's kernel_splitk
 // additionally required topk % SPLIT_K == 0, kernel.py:512; uneven chunks are
 // fine here).  Either way a chunk never exceeds the layout's maximum, so very
@@ -64,14 +73,28 @@ void choose_splits(int64_t T, int64_t H, int64_t K, int32_t requested, int32_t *
     if (S < min_s) S = min_s;
     c = ceil_div(K, S);
   } else {
-    // one workgroup covers up to 8 head groups (128 heads)
     const int64_t groups = H / dsa::kHeadsPerGroup > 0 ? H / dsa::kHeadsPerGroup : 1;
-    const int64_t units = (T > 0 ? T : 1) * ceil_div(groups, 8);
+    const int64_t Tn = T > 0 ? T : 1;
     const int64_t tiles = ceil_div(K, dsa::kKeysPerTile);
-    const bool wave_layout = dsa::attn_merges_in_kernel((int)H);
-    const int64_t max_s = wave_layout ? std::min<int64_t>(ceil_div(K, 64), kMaxWaveSplits)
-                                      : ceil_div(tiles, dsa::kMinTilesPerSplit);
-    S = ceil_div(dsa::kNumCU, units);
+    int64_t max_s;
+    if (groups % 2 != 0) {
+      // four-wave layout, merged in the kernel
+      S = ceil_div(dsa::kNumCU, Tn * ceil_div(groups, 8));
+      max_s = std::min<int64_t>(ceil_div(K, 64), kMaxWaveSplits);
+    } else if (Tn * groups <= dsa::kNumCU / 2) {
+      // four-wave layout, T x S x groups workgroups within one round
+      S = dsa::kNumCU / (Tn * groups);
+      max_s = std::min<int64_t>(ceil_div(K, 128), kMaxEvenWaveSplits);
+    } else if (groups % 8 == 0 && Tn * (groups / 4) <= dsa::kNumCU / 2) {
+      // workgroups of four head groups, within one round
+      S = dsa::kNumCU / (Tn * (groups / 4));
+      max_s = ceil_div(tiles, dsa::kMinTilesPerSplit);
+    } else {
+      // workgroups of 8 (groups % 8 == 0), 4 or 2 head groups
+      const int64_t per = groups % 8 == 0 ? 8 : groups % 4 == 0 ? 4 : 2;
+      S = ceil_div(dsa::kNumCU, Tn * (groups / per));
+      max_s = ceil_div(tiles, dsa::kMinTilesPerSplit);
+    }
     if (S > max_s) S = max_s;
     if (S < min_s) S = min_s;
     if (S < 1) S = 1;

@@ -1577,6 +1577,11 @@ hipError_t launch_wave(const AttnParams &p, int head_blocks, hipStream_t stream)
 
 bool attn_merges_in_kernel(int H) { return (H / kHeadsPerGroup) % 2 != 0; }  // the <8, 8> layout
 
+bool attn_wave_layout(int64_t T, int H, int64_t S) {
+  const int groups = H / kHeadsPerGroup;
+  return groups % 2 != 0 || T * S * groups <= kNumCU;
+}
+
 int attn_max_chunk(int) {
   static_assert(Lds<1>::kMaxChunkKeys == Lds<8>::kMaxChunkKeys, "one chunk bound for every layout");
   return Lds<1>::kMaxChunkKeys;
@@ -1594,20 +1599,24 @@ hipError_t launch_attention_partial(const AttnParams &p, hipStream_t stream) {
   if (p.T == 0) return hipSuccess;
   const int groups = p.H / kHeadsPerGroup;
   const int hb = attn_head_blocks(p.H);
+  // Odd group counts, and even ones whose workgroups of one group fit the
+  // CUs in one round (small-T decode: H=128, top-k 2048, T=1 21.5 -> 14.1
+  // us, T=4 28.6 -> 19.2 us; H=64 T=8 24.9 -> 19.0 us): four independent
+  // waves per head group and chunk, no gathers shared between head groups.
+  if (attn_wave_layout(p.T, p.H, p.num_splits)) return launch_wave(p, groups, stream);
   if (groups % 8 == 0) {
-    // Few workgroups (small-T decode): four-wave workgroups of four head
-    // groups each -- twice the workgroups, each gathering the chunk's keys --
-    // finish sooner while that grid still fits the CUs in one round (H=128,
-    // top-k 2048: T=1 28.0 -> 21.4 us, T=8 34.2 -> 27.8 us; the same bits);
-    // past that the eight-wave workgroups' shared gathers win (T=16 42.4
-    // against 53.1 us).
+    // Four-wave workgroups of four head groups each -- twice the workgroups
+    // of the eight-wave layout, each gathering the chunk's keys -- finish
+    // sooner while that grid fits the CUs in one round (H=128, top-k 2048:
+    // T=16 with 8 splits 35.1 us against 41.7 us for eight-wave workgroups
+    // and 16 splits, T=32 with 4 splits 49.6 against 53.0 us; the same
+    // bits); past that the eight-wave workgroups' shared gathers win.
     if ((int64_t)p.T * p.num_splits * (groups / 4) <= kNumCU)
       return launch_ring<4, 1>(p, groups / 4, stream);
     return launch_ring<8, 1>(p, hb, stream);  // one wave per head group
   }
   if (groups % 4 == 0) return launch_ring<4, 1>(p, hb, stream);
-  if (groups % 2 == 0) return launch_ring<8, 4>(p, hb, stream);  // 2 groups x 4 slices
-  return launch_wave(p, hb, stream);                             // 1 group, 4 independent waves
+  return launch_ring<8, 4>(p, hb, stream);  // 2 groups x 4 slices
 }
 
 hipError_t launch_attention_merge(const AttnParams &p, hipStream_t stream) {

@@ -74,6 +74,11 @@ int attn_max_chunk(int H);
 // heads (the layout with 8 feature slices per head group); otherwise the
 // merge kernel runs and the counters are not touched.
 bool attn_merges_in_kernel(int H);
+// Whether a call of T tokens, H heads and S splits runs the four-wave layout
+// (one workgroup per 16-head group and chunk): always for an odd number of
+// head groups, for an even one while its T * S * groups workgroups fit the
+// CUs in one round.
+bool attn_wave_layout(int64_t T, int H, int64_t S);
 
 // Whole call: per-chunk attention, then (num_splits > 1) the merge.
 hipError_t launch_attention(const AttnParams &p, hipStream_t stream);

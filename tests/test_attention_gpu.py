@@ -400,7 +400,8 @@ def _heads(d, H, seed):
 
 
 @pytest.mark.parametrize("H,T,splits", [(16, 8, 0), (16, 8, 3), (16, 4, 17), (16, 3, 40),
-                                        (32, 6, 5), (48, 5, 3), (64, 4, 2), (128, 4, 2)])
+                                        (32, 6, 5), (48, 5, 3), (64, 4, 2), (128, 4, 2),
+                                        (32, 160, 2), (64, 80, 4), (128, 16, 16)])
 def test_in_kernel_merge_matches_merge_kernel_bitwise(H, T, splits):
     """The merge inside the attention kernel (per-wave arrival counters) gives
     the same bits as the separate merge kernel and as kernel_partial +
@@ -425,16 +426,19 @@ def test_in_kernel_merge_matches_merge_kernel_bitwise(H, T, splits):
         _assert_parity(out.cpu(), lse.cpu(), *_oracle(d), f"in-kernel merge splits={splits}")
 
 
-@pytest.mark.parametrize("H", [48, 64, 96, 256])
-def test_head_counts_match_oracle(H):
-    """Every kernel layout against the oracle: 3 groups of 16 heads (the
-    8-slice layout in 3 head blocks), 4 (one wave per group, 4 waves), 6 (2
-    groups x 4 slices in 3 head blocks) and 16 (one wave per group, 8 waves,
-    2 head blocks); the default split choice, with padding in one row."""
-    d = _heads(workloads.cfg2(T=3, seed=500 + H), H, seed=H)
+@pytest.mark.parametrize("H,T", [(48, 3), (64, 3), (96, 3), (256, 3), (64, 80), (96, 48),
+                                 (256, 16), (256, 40)])
+def test_head_counts_match_oracle(H, T):
+    """Every kernel layout against the oracle, with the default split
+    choice and padding in one row: at T=3 the four-wave layout for 3, 4, 6
+    and 16 groups of 16 heads (odd and even counts); then 4 groups at T=80
+    (one wave per group, four-wave workgroups), 6 groups at T=48 (2 groups x
+    4 slices, 3 head blocks), 16 groups at T=16 (four-wave workgroups, 4 head
+    blocks) and at T=40 (eight-wave workgroups, 2 head blocks)."""
+    d = _heads(workloads.cfg2(T=T, seed=500 + H + T), H, seed=H + T)
     d["sparse_indices"] = d["sparse_indices"][:, :700].clone()
     d["sparse_indices"][1, 650:] = -1
-    print(f"head count H={H}", flush=True)
+    print(f"head count H={H} T={T}", flush=True)
     out, lse = _run(kernel, d)
     _assert_parity(out, lse, *_oracle(d), f"H={H}")
 
@@ -469,23 +473,24 @@ def test_sorted_and_unsorted_waves_in_one_workgroup(K):
 
 
 def test_h128_small_grid_layout_same_bits():
-    """H = 128 calls whose grid is small (here T=8 with 4 chunks) run four-wave
-    workgroups of 64 heads; larger ones (T=40) eight-wave workgroups of 128
-    heads.  The eight tokens give the same bits either way (same chunks, the
-    same arithmetic per head group), and match the oracle."""
+    """H = 128 calls whose ring grid fits the CUs in one round (here T=16 with
+    4 chunks) run four-wave workgroups of 64 heads; larger ones (T=40)
+    eight-wave workgroups of 128 heads.  The sixteen tokens give the same
+    bits either way (same chunks, the same arithmetic per head group), and
+    match the oracle."""
     T, H, K = 40, 128, 700
     d = workloads.attention_inputs(T, H, K, 64, 64, seed=4242)
     g = d.pop("gen")
     idx = torch.stack([torch.randperm(64 * 64, generator=g)[:K] for _ in range(T)]).to(torch.int32)
     idx[3, 600:] = -1
     d.update(sparse_indices=idx, sm_scale=0.0721)
-    print("H=128 layouts: T=8 and T=40, 4 chunks", flush=True)
+    print("H=128 layouts: T=16 and T=40, 4 chunks", flush=True)
     out_all, lse_all = _run(kernel_splitk, d, SPLIT_K=4)
-    small = dict(d, q_nope=d["q_nope"][:8].clone(), q_pe=d["q_pe"][:8].clone(),
-                 sparse_indices=idx[:8].clone())
-    out8, lse8 = _run(kernel_splitk, small, SPLIT_K=4)
-    assert torch.equal(out8, out_all[:8]) and torch.equal(lse8, lse_all[:8])
-    _assert_parity(out8, lse8, *_oracle(small), "H=128 T=8")
+    small = dict(d, q_nope=d["q_nope"][:16].clone(), q_pe=d["q_pe"][:16].clone(),
+                 sparse_indices=idx[:16].clone())
+    out16, lse16 = _run(kernel_splitk, small, SPLIT_K=4)
+    assert torch.equal(out16, out_all[:16]) and torch.equal(lse16, lse_all[:16])
+    _assert_parity(out16, lse16, *_oracle(small), "H=128 T=16")
 
 
 @pytest.mark.parametrize("case", range(12))
@@ -521,12 +526,15 @@ def test_random_shapes_match_oracle(case):
     _assert_parity(out, lse, *_oracle(dict(d, sparse_indices=clean)), f"random case {case}")
 
 
-@pytest.mark.parametrize("H,T", [(16, 4), (48, 2), (32, 4), (64, 4), (128, 4), (128, 16), (128, 64)])
-def test_every_layout_after_nan_filled_lds(H, T):
-    """Each kernel layout (four independent waves; 2 groups x 4 slices; one
-    wave per group in four-wave workgroups, small and large H=128 grids; the
-    two-team eight-wave layout at T=16 with 16 chunks and at T=64) runs right
-    after a kernel that left NaN in every CU's LDS.  Every LDS location a
+@pytest.mark.parametrize("H,T,splits", [(16, 4, 0), (48, 2, 0), (32, 4, 0), (128, 4, 0),
+                                        (32, 160, 0), (64, 80, 0), (128, 64, 0), (128, 16, 16),
+                                        (128, 64, 4)])
+def test_every_layout_after_nan_filled_lds(H, T, splits):
+    """Each kernel layout (four independent waves, for odd and even group
+    counts; 2 groups x 4 slices at H=32 T=160; one wave per group in
+    four-wave workgroups at H=64 T=80 and H=128 T=64; the two-team
+    eight-wave layout at H=128 T=16 with 16 chunks and T=64 with 4) runs
+    right after a kernel that left NaN in every CU's LDS.  Every LDS location a
     workgroup reads must have been written by its own gathers or stores
     before the read: a stage read before all waves' gathers of it landed
     turns the output NaN.  Several calls per shape, each on freshly
@@ -543,8 +551,9 @@ def test_every_layout_after_nan_filled_lds(H, T):
     for r in range(6):
         print(f"NaN-filled LDS H={H} T={T} call {r}", flush=True)
         fill_lds_with_nan(DEV)
-        out, lse = kernel(gd["q_nope"], gd["q_pe"], gd["ckv_cache"], gd["kpe_cache"],
-                          gd["sparse_indices"], d["sm_scale"])
+        a = (gd["q_nope"], gd["q_pe"], gd["ckv_cache"], gd["kpe_cache"], gd["sparse_indices"],
+             d["sm_scale"])
+        out, lse = kernel_splitk(*a, SPLIT_K=splits) if splits else kernel(*a)
         torch.cuda.synchronize()
         _assert_parity(out.cpu(), lse.cpu(), *ref, f"H={H} T={T} call {r}")
 
