@@ -287,10 +287,16 @@ def measure_attention(name, d, steps, warmup, cold_copies=0):
     # split merge inside the attention kernel) is that launch; otherwise the
     # gather-attention launch is timed alone and the merge kernel is the rest.
     splits = num_splits(T, H, K)
-    one_launch = splits == 1 or _lib.load().dsa_attn_counter_bytes(T, H) > 0
-    # H = 16 x an odd number: four independent waves per head group; else the
+    groups = H // 16
+    # kernel() brings split counters; the library merges inside the attention
+    # kernel where they exist (odd group counts) and the call has at most 4
+    # splits
+    one_launch = splits == 1 or (_lib.load().dsa_attn_counter_bytes(T, H) > 0 and splits <= 4)
+    # four independent waves per head group for odd group counts and for even
+    # ones whose T x splits x groups workgroups fit the 256 CUs; else the
     # shared-ring layout
-    kname = "dsa_attn_wave_kernel" if (H // 16) % 2 else "dsa_attn_ring_kernel"
+    kname = ("dsa_attn_wave_kernel" if groups % 2 or T * splits * groups <= 256
+             else "dsa_attn_ring_kernel")
     if one_launch:
         ms_dom = ms
         kdesc = (f"{kname} (gather attention"

@@ -36,24 +36,21 @@ bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-constexpr int64_t kMaxWaveSplits = 8;
-constexpr int64_t kMaxEvenWaveSplits = 16;
+constexpr int64_t kMaxWaveSplits = 16;
 
 // Top-k chunk length per split and the split count that results.  Automatic
 // mode aims for about one workgroup per compute unit while keeping enough
-// work per chunk: four 32-key tiles for the shared-ring layouts; for the
-// four-wave layout with an odd number of 16-head groups one 16-key block per
-// wave, and at most kMaxWaveSplits splits (measured at H=16, top-k 2048:
-// with 8 splits T = 1..16 run 1-3 us faster than with 16, whose longer
-// in-kernel merge outweighs their parallelism; at T = 64, 4 splits).  An
-// even number of groups takes the four-wave layout while T x groups <= 128,
-// with the most splits that keep its T x S x groups workgroups within one
-// round (chunks of at least 128 keys, at most kMaxEvenWaveSplits: 16 beat 8
-// by 1-2 us at T = 1..4 there, the separate merge kernel being cheap);
-// past that the shared-ring layouts, with the split count that fills one
-// round of their workgroups (H=128, top-k 2048, measured over T = 1..64 and
-// every layout and split count: the fastest configuration of each shape was
-// within 1.5 us of a grid of about one workgroup per CU).  An explicit
+// work per chunk: four 32-key tiles for the shared-ring layouts.  The
+// four-wave layout (every odd number of 16-head groups; an even number while
+// T x groups <= 128) takes the most splits that keep its T x S x groups
+// workgroups within one round, at most kMaxWaveSplits and chunks of at least
+// 64 keys (one 16-key block per wave).  Past that the shared-ring layouts,
+// with the split count that fills one round of their workgroups.  Measured
+// over H = 16..128, T = 1..64, every layout and split count (top-k 2048, and
+// 256 for config 1): the fastest configuration of each shape was within
+// about 1 us of a grid of about one workgroup per CU (H=16: T=1 16.3 -> 11.9
+// us with 16 splits instead of 8; H=48 T=64 82.5 -> 54.6 us with 1 split
+// instead of 4).  An explicit
 // request is honoured up to one key per split (the reference's kernel_splitk
 // additionally required topk % SPLIT_K == 0, kernel.py:512; uneven chunks are
 // fine here).  Either way a chunk never exceeds the layout's maximum, so very
@@ -77,14 +74,10 @@ void choose_splits(int64_t T, int64_t H, int64_t K, int32_t requested, int32_t *
     const int64_t Tn = T > 0 ? T : 1;
     const int64_t tiles = ceil_div(K, dsa::kKeysPerTile);
     int64_t max_s;
-    if (groups % 2 != 0) {
-      // four-wave layout, merged in the kernel
-      S = ceil_div(dsa::kNumCU, Tn * ceil_div(groups, 8));
-      max_s = std::min<int64_t>(ceil_div(K, 64), kMaxWaveSplits);
-    } else if (Tn * groups <= dsa::kNumCU / 2) {
+    if (groups % 2 != 0 || Tn * groups <= dsa::kNumCU / 2) {
       // four-wave layout, T x S x groups workgroups within one round
       S = dsa::kNumCU / (Tn * groups);
-      max_s = std::min<int64_t>(ceil_div(K, 128), kMaxEvenWaveSplits);
+      max_s = std::min<int64_t>(ceil_div(K, 64), kMaxWaveSplits);
     } else if (groups % 8 == 0 && Tn * (groups / 4) <= dsa::kNumCU / 2) {
       // workgroups of four head groups, within one round
       S = dsa::kNumCU / (Tn * (groups / 4));
@@ -143,7 +136,7 @@ size_t dsa_attn_workspace_bytes(int64_t num_tokens, int64_t num_heads, int64_t t
 
 size_t dsa_attn_counter_bytes(int64_t num_tokens, int64_t num_heads) {
   if (num_tokens <= 0 || num_heads < dsa::kHeadsPerGroup || num_heads > 4096 ||
-      !dsa::attn_merges_in_kernel((int)num_heads))
+      !dsa::attn_merges_in_kernel((int)num_heads, 2))
     return 0;
   return (size_t)dsa::attn_counter_words(num_tokens, dsa::attn_head_blocks((int)num_heads)) *
          sizeof(uint32_t);
@@ -203,7 +196,7 @@ int prepare_attn(const char *fn, const dsa_attn_args *a, bool partial_only, dsa:
     return fail(DSA_EWORKSPACE, "%s: workspace of %zu bytes (16-byte aligned) needed, got %zu",
                 fn, need, a->workspace ? a->workspace_bytes : (size_t)0);
   const bool merge_in_kernel = !partial_only && S > 1 && a->split_counters != nullptr &&
-                               dsa::attn_merges_in_kernel((int)a->num_heads);
+                               dsa::attn_merges_in_kernel((int)a->num_heads, S);
   if (merge_in_kernel) {
     const size_t cneed = (size_t)dsa::attn_counter_words(
                              a->num_tokens, dsa::attn_head_blocks((int)a->num_heads)) *

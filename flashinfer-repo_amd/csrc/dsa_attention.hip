@@ -1575,7 +1575,9 @@ hipError_t launch_wave(const AttnParams &p, int head_blocks, hipStream_t stream)
 
 }  // namespace
 
-bool attn_merges_in_kernel(int H) { return (H / kHeadsPerGroup) % 2 != 0; }  // the <8, 8> layout
+bool attn_merges_in_kernel(int H, int64_t S) {
+  return (H / kHeadsPerGroup) % 2 != 0 && S <= kMaxInKernelMergeSplits;
+}
 
 bool attn_wave_layout(int64_t T, int H, int64_t S) {
   const int groups = H / kHeadsPerGroup;
@@ -1631,7 +1633,7 @@ hipError_t launch_attention_merge(const AttnParams &p, hipStream_t stream) {
 
 hipError_t launch_attention(const AttnParams &pin, hipStream_t stream) {
   AttnParams p = pin;
-  if (!attn_merges_in_kernel(p.H)) p.counters = nullptr;
+  if (!attn_merges_in_kernel(p.H, p.num_splits)) p.counters = nullptr;
   hipError_t e = launch_attention_partial(p, stream);
   if (e != hipSuccess || (p.num_splits == 1 && !p.partial_only) || p.counters != nullptr) return e;
   return launch_attention_merge(p, stream);

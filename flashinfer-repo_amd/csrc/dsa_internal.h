@@ -71,9 +71,15 @@ int attn_head_blocks(int H);
 // Longest top-k chunk one workgroup of the layout for H heads handles.
 int attn_max_chunk(int H);
 // Whether split calls with counters merge inside the attention kernel for H
-// heads (the layout with 8 feature slices per head group); otherwise the
-// merge kernel runs and the counters are not touched.
-bool attn_merges_in_kernel(int H);
+// heads and S splits: the four-wave layout of an odd number of head groups,
+// up to kMaxInKernelMergeSplits splits (the last chunk's wave reads every
+// chunk's partial; from 5 splits on the merge kernel, which spreads that
+// work over the tokens and heads, is faster: H=16 top-k 2048, 8 splits, T=1
+// 16.3 against 14.5 us, T=32 22.6 against 21.7 us; at 4 splits the in-kernel
+// merge is as fast or faster and saves a launch).  Otherwise the merge kernel
+// runs and the counters are not touched.
+constexpr int kMaxInKernelMergeSplits = 4;
+bool attn_merges_in_kernel(int H, int64_t S);
 // Whether a call of T tokens, H heads and S splits runs the four-wave layout
 // (one workgroup per 16-head group and chunk): always for an odd number of
 // head groups, for an even one while its T * S * groups workgroups fit the

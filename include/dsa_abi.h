@@ -75,8 +75,9 @@ extern "C" {
  * split call runs a second kernel that merges the partials (the reference's
  * kernel_splitk launch pair, kernel.py:534 and :555).  Where
  * dsa_attn_counter_bytes() is not 0 (head counts of an odd number of 16-head
- * groups, e.g. H=16 decode) and that much 4-byte aligned, all-zero memory is
- * given, the merge happens inside the attention kernel instead (the
+ * groups, e.g. H=16 decode), the call has at most 4 splits (more are merged
+ * faster by the second kernel) and that much 4-byte aligned, all-zero memory
+ * is given, the merge happens inside the attention kernel instead (the
  * workgroup that finishes a token's chunk last merges it; same bits as the
  * two-kernel path) and every call that completes leaves the counters zero
  * again, so zero them once (e.g. hipMemset) and reuse them for calls of any

@@ -66,12 +66,21 @@ def test_split_choice():
     assert lib.dsa_attn_num_splits(64, 128, 4096, 1) == 2      # ... and no longer
     assert lib.dsa_attn_num_splits(2048, 16, 1024, 0) == 1     # prefill needs no split
     assert lib.dsa_attn_num_splits(8, 16, 4096, 1) == 2        # requests below the minimum are raised
-    # four-wave layout (H = 16 x odd): at most 8 splits, >= one 16-key block per wave
-    assert lib.dsa_attn_num_splits(1, 16, 2048, 0) == 8
-    assert lib.dsa_attn_num_splits(16, 16, 2048, 0) == 8
+    # four-wave layout (H = 16 x odd, or x even while T x groups <= 128): the
+    # most splits whose T x S x groups workgroups fit 256 CUs, at most 16,
+    # >= one 16-key block per wave
+    assert lib.dsa_attn_num_splits(1, 16, 2048, 0) == 16
+    assert lib.dsa_attn_num_splits(16, 16, 2048, 0) == 16
+    assert lib.dsa_attn_num_splits(32, 16, 2048, 0) == 8
+    assert lib.dsa_attn_num_splits(8, 48, 2048, 0) == 10        # 24 x 10 = 240 workgroups
+    assert lib.dsa_attn_num_splits(64, 48, 2048, 0) == 1
     assert lib.dsa_attn_num_splits(4, 16, 256, 0) == 4          # 64 keys per split
     assert lib.dsa_attn_num_splits(1, 16, 32768, 0) == 16       # 2048-key chunks at most
-    assert lib.dsa_attn_num_splits(1, 32, 2048, 0) == 16        # shared-ring layout: 4 tiles per split
+    assert lib.dsa_attn_num_splits(1, 32, 2048, 0) == 16
+    assert lib.dsa_attn_num_splits(4, 128, 2048, 0) == 8        # 4 x 8 x 8 = 256
+    # shared-ring layouts: one round of their workgroups
+    assert lib.dsa_attn_num_splits(64, 128, 2048, 0) == 2       # 64 x 2 workgroups of 4 groups
+    assert lib.dsa_attn_num_splits(128, 32, 2048, 0) == 2       # 2 groups x 4 slices
     assert lib.dsa_attn_num_splits(64, 16, 2048, 16) == 16     # explicit request honoured
     assert lib.dsa_attn_num_splits(1, 16, 5, 128) == 5         # at most one key per split
     assert lib.dsa_attn_num_splits(4, 16, 0, 0) == 1

@@ -401,11 +401,14 @@ def _heads(d, H, seed):
 
 @pytest.mark.parametrize("H,T,splits", [(16, 8, 0), (16, 8, 3), (16, 4, 17), (16, 3, 40),
                                         (32, 6, 5), (48, 5, 3), (64, 4, 2), (128, 4, 2),
-                                        (32, 160, 2), (64, 80, 4), (128, 16, 16)])
+                                        (32, 160, 2), (64, 80, 4), (128, 16, 16), (16, 64, 0),
+                                        (48, 16, 4)])
 def test_in_kernel_merge_matches_merge_kernel_bitwise(H, T, splits):
-    """The merge inside the attention kernel (per-wave arrival counters) gives
-    the same bits as the separate merge kernel and as kernel_partial +
-    merge_partials, for every kernel layout, and leaves its counters zero."""
+    """The merge inside the attention kernel (per-wave arrival counters; odd
+    group counts with at most 4 splits) gives the same bits as the separate
+    merge kernel and as kernel_partial + merge_partials, and leaves its
+    counters zero; calls that merge with the separate kernel (more splits, even
+    group counts, every layout) give the same bits through every entry."""
     d = _heads(workloads.cfg2(T=T, seed=90 + H), H, seed=H * 7 + T)
     g = workloads.to_device(d, DEV)
     args = (g["q_nope"], g["q_pe"], g["ckv_cache"], g["kpe_cache"], g["sparse_indices"],
@@ -561,9 +564,12 @@ def test_every_layout_after_nan_filled_lds(H, T, splits):
 def test_in_kernel_merge_counters_reused_across_calls_and_shapes():
     """One counter buffer serves consecutive calls of different shapes and
     split counts; each result equals the merge-kernel path."""
-    big = workloads.to_device(workloads.cfg2(T=16, seed=301), DEV)
-    cnt = new_split_counters(big["q_nope"])
-    cases = [(16, 16, 301, 0), (3, 48, 302, 5), (16, 16, 303, 4), (1, 16, 304, 0), (9, 32, 305, 7)]
+    big = workloads.to_device(workloads.cfg2(T=64, seed=301), DEV)
+    cnt = new_split_counters(big["q_nope"])  # sized for the largest case below
+    # odd group counts with at most 4 splits merge in the kernel; the rest
+    # (8 splits, an even group count) leave the counters alone
+    cases = [(16, 16, 301, 2), (3, 48, 302, 3), (16, 16, 303, 4), (1, 16, 304, 8), (9, 32, 305, 7),
+             (64, 16, 306, 0), (2, 48, 307, 4)]
     for T, H, seed, splits in cases:
         d = _heads(workloads.cfg2(T=T, seed=seed), H, seed=seed)
         g = workloads.to_device(d, DEV)
@@ -582,7 +588,7 @@ def test_in_kernel_merge_graph_replays():
     """A graph captured on a stream whose counters an eager call already made
     merges in-kernel; every replay (new queries copied in between, eager work
     and synchronisation between replays) equals the merge-kernel path."""
-    d = workloads.cfg2(T=24, seed=311)
+    d = workloads.cfg2(T=64, seed=311)  # 4 splits: merged in the kernel
     g = workloads.to_device(d, DEV)
     args = (g["q_nope"], g["q_pe"], g["ckv_cache"], g["kpe_cache"], g["sparse_indices"],
             d["sm_scale"])
@@ -612,7 +618,7 @@ def test_captured_counters_outlive_a_larger_eager_call():
     counters are not the ones eager calls on its stream use."""
     import importlib
     kmod = importlib.import_module("dsa_amd.kernel")
-    d = workloads.cfg2(T=24, seed=321)
+    d = workloads.cfg2(T=64, seed=321)  # 4 splits: merged in the kernel
     g = workloads.to_device(d, DEV)
     args = (g["q_nope"], g["q_pe"], g["ckv_cache"], g["kpe_cache"], g["sparse_indices"],
             d["sm_scale"])
