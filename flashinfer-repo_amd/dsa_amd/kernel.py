@@ -48,11 +48,12 @@ def new_workspace(q_nope: torch.Tensor, topk: int, num_splits: int = 0) -> torch
 
 def new_split_counters(q_nope: torch.Tensor) -> torch.Tensor:
     """Zeroed merge counters for calls of up to ``q_nope``'s token and head
-    counts (pass to :func:`kernel_out`).  Split calls of head counts with an
-    odd number of 16-head groups (e.g. H=16 decode) that are given them merge
-    their chunks inside the attention kernel and leave them zero again (other
-    head counts ignore them); calls that may run at the same time (other
-    streams, graphs replayed concurrently) each need their own."""
+    counts (pass to :func:`kernel_out`).  Calls of head counts with an odd
+    number of 16-head groups (e.g. H=16 decode) and 2 to 4 splits that are
+    given them merge their chunks inside the attention kernel and leave them
+    zero again (other calls ignore them and run the merge kernel); calls that
+    may run at the same time (other streams, graphs replayed concurrently)
+    each need their own."""
     T, H, _ = q_nope.shape
     nbytes = _lib.load().dsa_attn_counter_bytes(T, H)
     return torch.zeros(max(nbytes // 4, 1), dtype=torch.int32, device=q_nope.device)
