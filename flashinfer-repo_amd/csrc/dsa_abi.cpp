@@ -42,7 +42,7 @@ constexpr int64_t kMaxWaveSplits = 16;
 // mode aims for about one workgroup per compute unit while keeping enough
 // work per chunk: four 32-key tiles for the shared-ring layouts.  The
 // four-wave layout (every odd number of 16-head groups; an even number while
-// T x groups <= 128) takes the most splits that keep its T x S x groups
+// T x groups <= 128, or <= 64 for multiples of 8 groups) takes the most splits that keep its T x S x groups
 // workgroups within one round, at most kMaxWaveSplits and chunks of at least
 // 64 keys (one 16-key block per wave).  Past that the shared-ring layouts,
 // with the split count that fills one round of their workgroups.  Measured
@@ -74,7 +74,10 @@ void choose_splits(int64_t T, int64_t H, int64_t K, int32_t requested, int32_t *
     const int64_t Tn = T > 0 ? T : 1;
     const int64_t tiles = ceil_div(K, dsa::kKeysPerTile);
     int64_t max_s;
-    if (groups % 2 != 0 || Tn * groups <= dsa::kNumCU / 2) {
+    // the four-wave layout while it gets at least 2 splits (at least 4 for
+    // multiples of 8 groups, whose four-wave ring layout is faster at 2:
+    // H=128 T=16 35.1 us with 8 splits against 36.8 us)
+    if (groups % 2 != 0 || Tn * groups <= dsa::kNumCU / (groups % 8 == 0 ? 4 : 2)) {
       // four-wave layout, T x S x groups workgroups within one round
       S = dsa::kNumCU / (Tn * groups);
       max_s = std::min<int64_t>(ceil_div(K, 64), kMaxWaveSplits);
