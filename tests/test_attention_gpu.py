@@ -104,9 +104,18 @@ def test_cfg3_prefill_full():
 
 
 def test_cfg4_h128_outliers_full():
+    """Config 4 (H=128, 5 % of the cache rows scaled by 8) in one chunk per
+    token, and split into 2 and 4 chunks merged by the merge kernel (outputs
+    reach 16-32, where one bf16 step is 0.125: the split results may differ
+    from the unsplit ones by a step, within the checker's relative bound)."""
     d = workloads.cfg4()
+    ref = _oracle(d)
     out, lse = _run(kernel, d)
-    _assert_parity(out, lse, *_oracle(d), "cfg4")
+    _assert_parity(out, lse, *ref, "cfg4")
+    for splits in (2, 4):
+        print(f"cfg4 with {splits} splits", flush=True)
+        out, lse = _run(kernel_splitk, d, SPLIT_K=splits)
+        _assert_parity(out, lse, *ref, f"cfg4 {splits} splits")
 
 
 @pytest.mark.parametrize("K", [1, 5, 31, 32, 33, 100, 257])
