@@ -56,6 +56,9 @@ INT8_PEAK_TOPS = 5000.0      # dense int8 MFMA (= the fp8 dense peak)
 GRAPH_CALLS = 20
 EXTRA_STEPS = 100            # timed calls per extra workload of the default run
 ATTN_CONFIGS = ("cfg1", "cfg2", "cfg3", "cfg4", "t1")
+# Workloads whose cache fits the 256 MB Infinity Cache also get a cold-cache
+# figure: calls rotating through this many copies of the cache.
+COLD_COPIES = {"cfg2": 3, "cfg4": 4}
 
 # The reference's published T=1 figures (RTX 6000 Ada, docs/PROFILING.md:47-48,
 # docs/SPLITK_OPTIMIZATION.md:140-148,159-163) -- context for the t1 workload.
@@ -75,11 +78,21 @@ def parse():
                          "carried in the line)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cold-copies", type=int, default=-1, metavar="N",
-                    help="also time cfg2 calls rotating through N copies of the KV cache "
-                         "(default 3: 453 MB, beyond the 256 MB Infinity Cache; 0 = off)")
+                    help="also time calls rotating through N copies of the KV cache "
+                         "(default: cfg2 3 copies, 453 MB, and cfg4 4 copies, 302 MB, beyond "
+                         "the 256 MB Infinity Cache; 0 = off)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run 5 plain device copies of BYTES bytes (the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
+    ap.add_argument("--record-profiles", default=None, metavar="OUT_DIR",
+                    help="run rocprofv3 over --config X of every workload (kernel trace, then "
+                         "one counter pass each: FETCH_SIZE, WRITE_SIZE, MFMA busy, L2 hits) "
+                         "and the copy calibration, raw output under OUT_DIR; write "
+                         "profiles/traffic.json (with the kernel sources' hash) and one "
+                         "summary per workload under profiles/ (this process never touches "
+                         "the GPU)")
+    ap.add_argument("--profile-configs", default=",".join(ATTN_CONFIGS + ("cfg5",)),
+                    help="workloads --record-profiles covers (comma-separated)")
     return ap.parse_args()
 
 
@@ -153,28 +166,33 @@ def host_cpu():
     return model, os.cpu_count()
 
 
-def cpu_baseline(d):
+def cpu_baseline(d, budget_s: float = 20.0):
     """The torch fp32 restatement of run() (oracle/torch_ref.py) on the host:
-    1 warm-up and 3 timed whole calls, median."""
+    1 warm-up and up to 3 timed whole calls, median; fewer timed calls when
+    the calls so far have used up ``budget_s`` (the long prefill shapes)."""
     import torch
 
     from oracle.torch_ref import run_fp32
     threads = torch.get_num_threads()   # the box's CPU share (OMP_NUM_THREADS) of the host
     args = (d["q_nope"], d["q_pe"], d["ckv_cache"], d["kpe_cache"], d["sparse_indices"],
             d["sm_scale"])
+    t0 = time.perf_counter()
     run_fp32(*args)
+    spent = time.perf_counter() - t0
     times = []
-    for _ in range(3):
+    while len(times) < 3 and (not times or spent + times[-1] <= budget_s):
         t0 = time.perf_counter()
         run_fp32(*args)
         times.append(time.perf_counter() - t0)
+        spent += times[-1]
     times.sort()
     model, ncpu = host_cpu()
     T = d["q_nope"].shape[0]
-    return {"value": round(times[1] * 1e6, 1), "unit": "µs/call", "cores": threads, "kind": "port",
+    return {"value": round(times[len(times) // 2] * 1e6, 1), "unit": "µs/call", "cores": threads,
+            "kind": "port",
             "sample": f"whole {T}-token calls of the torch fp32 restatement of run() "
                       f"(indexer_kernel.py:436-497: whole-cache fp32 conversion, per-token "
-                      f"loop), median of 3 after 1 warm-up: "
+                      f"loop), median of {len(times)} after 1 warm-up: "
                       f"{', '.join(f'{x:.3f}' for x in times)} s",
             "host": {"lscpu_model": model, "logical_cpus": ncpu, "torch_threads": threads}}
 
@@ -291,7 +309,7 @@ def measure_attention(name, d, steps, warmup, cold_copies=0):
     # kernel() brings split counters; the library merges inside the attention
     # kernel where they exist (odd group counts) and the call has at most 4
     # splits
-    one_launch = splits == 1 or (_lib.load().dsa_attn_counter_bytes(T, H) > 0 and splits <= 4)
+    one_launch = splits == 1 or _lib.load().dsa_attn_call_counter_bytes(T, H, K, 0) > 0
     # four independent waves per head group for odd group counts and for even
     # ones whose T x splits x groups workgroups fit the 256 CUs; else the
     # shared-ring layout
@@ -332,7 +350,10 @@ def measure_attention(name, d, steps, warmup, cold_copies=0):
                 "cache_bytes_per_copy": (g["ckv_cache"].numel() + g["kpe_cache"].numel()) * 2,
                 "us_per_call": round(ms_cold * 1e3, 3),
                 "gathered_GBps": round(alg_bytes / (ms_cold * 1e-3) / 1e9, 1),
-                "frac_of_hbm_peak": round(alg_bytes / (ms_cold * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+                "frac_of_hbm_peak": round(alg_bytes / (ms_cold * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "TFLOPs": round(alg_flops / (ms_cold * 1e-3) / 1e12, 2),
+                "frac_of_bf16_peak": round(alg_flops / (ms_cold * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+                                           5)}
         del copies
 
     gbs = alg_bytes / (ms_dom * 1e-3) / 1e9
@@ -444,10 +465,163 @@ ATTN_DATA = "synthetic (seeded; q~N(0,1), cache~N(0,0.5), distinct slots per tok
 IDX_DATA = "synthetic (seeded; q_idx,k_idx ~N(0,1) as e4m3, scale~U(0.5,2), w~N(0,1/8))"
 
 
+# ---- rocprofv3 records ------------------------------------------------------
+
+PROFILE_STEPS = ["--steps", "40", "--warmup", "5", "--no-cpu-baseline", "--cold-copies", "0"]
+COUNTER_PASSES = (("FETCH_SIZE",), ("WRITE_SIZE",),
+                  ("SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CU_CYCLES", "SQ_INSTS_MFMA"),
+                  ("TCC_HIT_sum", "TCC_MISS_sum"))
+CALIBRATION_BYTES = 1 << 28
+
+
+def _short_name(name: str) -> str:
+    """Kernel name without namespaces and parameter list."""
+    base = name.split("(")[0]
+    return base.replace("void ", "").replace("dsa::(anonymous namespace)::", "").strip()
+
+
+def _dominant(config: str, names):
+    """The kernels that make up a workload's measured launch: for attention
+    the gather-attention kernel (not the merge kernel), for cfg5 the
+    per-call operand preparation plus the score kernel (the timed score
+    step)."""
+    if config == "cfg5":
+        return sorted(n for n in names if "dsa_idx_prep" in n or "dsa_idx_score" in n)
+    return [n for n in names if n.startswith("dsa_attn_") and "combine" not in n][:1]
+
+
+def _rocprof(args, out_dir, tag, program, log):
+    """One rocprofv3 run (its own process, under its own time limit); the
+    program follows ``--``."""
+    cmd = ["timeout", "-s", "KILL", "180", "rocprofv3", *args, "-d", os.path.join(out_dir, tag),
+           "-o", "run", "--output-format", "csv", "--", *program]
+    print(f"record: {tag}: {' '.join(cmd)}", flush=True)
+    env = dict(os.environ, TMPDIR="/tmp")
+    with open(log, "w") as f:
+        r = subprocess.run(cmd, stdout=f, stderr=subprocess.STDOUT, cwd="/tmp", env=env)
+    if r.returncode != 0:
+        raise SystemExit(f"record: {tag} failed with status {r.returncode} (log {log})")
+    shown = ["python3", "bench.py"] + list(program[2:])
+    return " ".join(["rocprofv3", *args, "-d <out> -o run --output-format csv --", *shown])
+
+
+def _counters(path):
+    """{kernel: {counter: median over dispatches}} of a counter pass (values of
+    one dispatch summed over the counter's instances)."""
+    import collections
+    import csv
+    import statistics
+    per = collections.defaultdict(lambda: collections.defaultdict(float))
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            per[(r["Dispatch_Id"], _short_name(r["Kernel_Name"]))][r["Counter_Name"]] += \
+                float(r["Counter_Value"])
+    agg = collections.defaultdict(lambda: collections.defaultdict(list))
+    for (_, k), v in per.items():
+        for c, x in v.items():
+            agg[k][c].append(x)
+    return {k: {c: statistics.median(v) for c, v in d.items()} for k, d in agg.items()}
+
+
+def record_profiles(out_dir: str, configs) -> None:
+    """Runs the profiler over every workload and writes profiles/traffic.json
+    and profiles/<kernel>_<workload>.txt from what it measured."""
+    import csv
+    out_dir = os.path.abspath(out_dir)
+    os.makedirs(out_dir, exist_ok=True)
+    bench = [sys.executable, os.path.join(ROOT, "bench.py")]
+    calib = {}
+    cal_cmds = []
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        tag = f"pmc_{ctr}_copy"
+        cal_cmds.append(_rocprof(["--pmc", ctr], out_dir, tag,
+                                 bench + ["--copy-calibration", str(CALIBRATION_BYTES)],
+                                 os.path.join(out_dir, tag + ".log")))
+        vals = _counters(os.path.join(out_dir, tag, "run_counter_collection.csv"))
+        kib = max(v.get(ctr, 0.0) for k, v in vals.items() if "copy" in k.lower())
+        calib[ctr] = (CALIBRATION_BYTES / 1024.0) / kib  # KiB per KiB the counter reads
+    cal_note = (f"FETCH_SIZE x{calib['FETCH_SIZE']:.4f}, WRITE_SIZE x{calib['WRITE_SIZE']:.4f} "
+                f"(plain device copy of {CALIBRATION_BYTES} bytes)")
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            table = json.load(f)
+    except (OSError, ValueError):
+        table = {}
+    digest = csrc_hash()
+    for c in configs:
+        program = bench + PROFILE_STEPS + ["--config", c]
+        cmds = [_rocprof(["--kernel-trace", "--stats"], out_dir, f"trace_{c}", program,
+                         os.path.join(out_dir, f"trace_{c}.log"))]
+        stats = []
+        with open(os.path.join(out_dir, f"trace_{c}", "run_kernel_stats.csv")) as f:
+            for r in csv.DictReader(f):
+                stats.append((_short_name(r["Name"]), int(r["Calls"]), float(r["AverageNs"]) / 1e3,
+                              float(r["MinNs"]) / 1e3, float(r["MaxNs"]) / 1e3,
+                              float(r["Percentage"])))
+        dom = _dominant(c, [n for n, *_ in stats])
+        ctr = {}
+        for group in COUNTER_PASSES:
+            tag = f"pmc_{group[0]}_{c}"
+            cmds.append(_rocprof(["--pmc", *group], out_dir, tag, program,
+                                 os.path.join(out_dir, tag + ".log")))
+            vals = _counters(os.path.join(out_dir, tag, "run_counter_collection.csv"))
+            for k in dom:
+                for name, x in vals.get(k, {}).items():
+                    ctr[name] = ctr.get(name, 0.0) + x
+        fetch = ctr.get("FETCH_SIZE", 0.0) * 1024 * calib["FETCH_SIZE"]
+        write = ctr.get("WRITE_SIZE", 0.0) * 1024 * calib["WRITE_SIZE"]
+        busy = ctr.get("SQ_BUSY_CU_CYCLES", 0.0)
+        mfma = ctr.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / (4 * busy) if busy else None
+        hits, miss = ctr.get("TCC_HIT_sum", 0.0), ctr.get("TCC_MISS_sum", 0.0)
+        name = dom[-1] if dom else "none"
+        summary_file = f"{name.split('<')[0]}_{c}.txt"
+        dur = {n: avg for n, _, avg, *_ in stats}
+        table[c] = {
+            "kernel": " + ".join(dom),
+            "kernel_avg_us": round(sum(dur.get(k, 0.0) for k in dom), 3),
+            "fetch_bytes_per_launch": int(round(fetch)),
+            "write_bytes_per_launch": int(round(write)),
+            "hbm_bytes_per_launch": int(round(fetch + write)),
+            "mfma_busy_frac": round(mfma, 4) if mfma is not None else None,
+            "l2_hit_frac": round(hits / (hits + miss), 4) if hits + miss else None,
+            "calibration": cal_note,
+            "csrc_sha256": digest,
+            "source": f"profiles/{summary_file}",
+        }
+        lines = [f"rocprofv3 record of workload {c}: dominant launch {' + '.join(dom)}",
+                 f"kernel sources sha256 {digest} (bench.py csrc_hash)", "",
+                 "Commands (each its own run, from /tmp with TMPDIR=/tmp):"]
+        lines += [f"  {x}" for x in cmds + cal_cmds]
+        lines += ["", "Kernel trace (--kernel-trace --stats): calls, average / min / max us, share"]
+        for n, calls, avg, mn, mx, pct in stats:
+            if pct >= 0.5:
+                lines.append(f"  {n:70s} {calls:6d} {avg:10.3f} {mn:10.3f} {mx:10.3f} {pct:6.1f}%")
+        lines += ["", "Counters of the dominant launch (median per dispatch, summed over its "
+                      "kernels):"]
+        lines += [f"  {k:28s} {v:.6g}" for k, v in sorted(ctr.items())]
+        lines += ["", f"Calibration: {cal_note}",
+                  f"HBM bytes per launch: fetched {fetch:,.0f} + written {write:,.0f} = "
+                  f"{fetch + write:,.0f}",
+                  f"MFMA busy (SQ_VALU_MFMA_BUSY_CYCLES / (4 x SQ_BUSY_CU_CYCLES)): "
+                  + (f"{mfma:.4f}" if mfma is not None else "n/a"),
+                  "L2 hit (TCC_HIT / (TCC_HIT + TCC_MISS)): "
+                  + (f"{hits / (hits + miss):.4f}" if hits + miss else "n/a")]
+        with open(os.path.join(ROOT, "profiles", summary_file), "w") as f:
+            f.write("\n".join(lines) + "\n")
+        with open(path, "w") as f:
+            json.dump(table, f, indent=1)
+            f.write("\n")
+        print(f"record: {c}: {table[c]}", flush=True)
+
+
 def main():
     a = parse()
     if a.copy_calibration:
         copy_calibration(a.copy_calibration)
+        return
+    if a.record_profiles:
+        record_profiles(a.record_profiles, [c for c in a.profile_configs.split(",") if c])
         return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
@@ -472,7 +646,7 @@ def main():
 
     name = a.config or "cfg2"
     d = workloads.CONFIGS[name]()
-    cold = a.cold_copies if a.cold_copies >= 0 else (3 if name == "cfg2" else 0)
+    cold = a.cold_copies if a.cold_copies >= 0 else COLD_COPIES.get(name, 0)
     f = measure_attention(name, d, a.steps, a.warmup, cold)
     T, H, _ = d["q_nope"].shape
     K = d["sparse_indices"].shape[1]
@@ -489,12 +663,18 @@ def main():
         extra = {}
         for other in ("cfg1", "cfg3", "cfg4", "t1"):
             od = workloads.CONFIGS[other]()
-            extra[other] = summary(measure_attention(other, od, steps, warm))
+            # cfg4's 75.5 MB cache also fits the Infinity Cache: 4 copies (302 MB) rotate
+            extra[other] = summary(measure_attention(other, od, steps, warm,
+                                                     COLD_COPIES.get(other, 0)))
+            if not a.no_cpu_baseline:
+                extra[other]["cpu_baseline"] = cpu_baseline(od)
             del od
             torch.cuda.empty_cache()
         extra["t1"]["reference_published"] = T1_REFERENCE
-        fi, _ = measure_indexer(steps, warm)
+        fi, di = measure_indexer(steps, warm)
         extra["cfg5"] = summary(fi)
+        if not a.no_cpu_baseline:
+            extra["cfg5"]["cpu_baseline"] = cpu_indexer_baseline(di)
         line["workloads"] = extra
     print(json.dumps(line), flush=True)
 

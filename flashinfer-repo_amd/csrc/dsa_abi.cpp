@@ -145,6 +145,15 @@ size_t dsa_attn_counter_bytes(int64_t num_tokens, int64_t num_heads) {
          sizeof(uint32_t);
 }
 
+size_t dsa_attn_call_counter_bytes(int64_t num_tokens, int64_t num_heads, int64_t topk,
+                                   int32_t requested_splits) {
+  if (requested_splits < 0 || num_heads < dsa::kHeadsPerGroup || num_heads > 4096) return 0;
+  int32_t s, c;
+  choose_splits(num_tokens, num_heads, topk, requested_splits, &s, &c);
+  if (s < 2 || !dsa::attn_merges_in_kernel((int)num_heads, s)) return 0;
+  return dsa_attn_counter_bytes(num_tokens, num_heads);
+}
+
 }  // extern "C"
 
 namespace {

@@ -31,6 +31,7 @@ EXPORTED_SYMBOLS = (
     "dsa_attn_partial_bytes",
     "dsa_attn_workspace_bytes",
     "dsa_attn_counter_bytes",
+    "dsa_attn_call_counter_bytes",
     "dsa_indexer_topk",
     "dsa_indexer_k_append",
     "dsa_indexer_workspace_bytes",
@@ -140,6 +141,8 @@ def load() -> ctypes.CDLL:
     lib.dsa_attn_workspace_bytes.restype = ctypes.c_size_t
     lib.dsa_attn_counter_bytes.argtypes = [_i64, _i64]
     lib.dsa_attn_counter_bytes.restype = ctypes.c_size_t
+    lib.dsa_attn_call_counter_bytes.argtypes = [_i64, _i64, _i64, ctypes.c_int32]
+    lib.dsa_attn_call_counter_bytes.restype = ctypes.c_size_t
     lib.dsa_indexer_topk.argtypes = [ctypes.POINTER(IndexerArgs), _vp]
     lib.dsa_indexer_topk.restype = ctypes.c_int
     lib.dsa_indexer_k_append.argtypes = [ctypes.POINTER(KAppendArgs), _vp]

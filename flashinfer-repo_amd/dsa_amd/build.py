@@ -103,6 +103,15 @@ def build(verbose: bool = False, sanitize: bool = False) -> str:
     return LIB_PATH
 
 
+def build_test_support(src: str, lib: str, verbose: bool = False) -> str:
+    """Compile one self-contained HIP source of the tests (not part of the
+    product library) into its own shared object ``lib``."""
+    tmp = lib + ".tmp"
+    _run_all([[hipcc(), *COMMON_FLAGS, *OPT_FLAGS, "-shared", "-o", tmp, src]], verbose)
+    os.replace(tmp, lib)
+    return lib
+
+
 def sanitizer_runtime() -> str:
     """The AddressSanitizer runtime of ROCm's clang (to LD_PRELOAD into a
     process that loads libdsa_amd_san.so)."""

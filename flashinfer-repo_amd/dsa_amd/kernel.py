@@ -216,7 +216,9 @@ def _make_plan(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, num
     plan.template = bytes(a)
     plan.T, plan.H, plan.dev = T, H, dev
     plan.ws_bytes = lib.dsa_attn_workspace_bytes(T, H, K, int(num_splits))
-    plan.c_bytes = lib.dsa_attn_counter_bytes(T, H) if plan.ws_bytes else 0
+    # counters only for calls that merge their splits inside the attention
+    # kernel (the others run the merge kernel and never touch them)
+    plan.c_bytes = lib.dsa_attn_call_counter_bytes(T, H, K, int(num_splits)) if plan.ws_bytes else 0
     return plan
 
 
@@ -343,7 +345,7 @@ def _attention(q_nope, q_pe, ckv_cache, kpe_cache, sparse_indices, sm_scale, num
     a.lse, a.lse_stride_t, a.lse_stride_h = lse.data_ptr(), lse.stride(0), lse.stride(1)
     a.workspace = ws.data_ptr() if ws is not None else None
     a.workspace_bytes = ws_bytes
-    c_bytes = lib.dsa_attn_counter_bytes(T, H) if ws is not None else 0
+    c_bytes = lib.dsa_attn_call_counter_bytes(T, H, K, int(num_splits)) if ws is not None else 0
     if c_bytes:
         if split_counters is not None:
             _check_counters(split_counters, c_bytes, dev)

@@ -26,8 +26,10 @@
  *   dsa_indexer_k_append  no kernel in the reference: writes the paged fp8
  *                         indexer K cache that indexer_kernel.py:163-197
  *                         reads (quantise-on-append).
- *   dsa_attn_counter_bytes  no counterpart: size of the optional split
- *                         counters of dsa_attn_fwd.
+ *   dsa_attn_counter_bytes / dsa_attn_call_counter_bytes
+ *                         no counterpart: size of the optional split
+ *                         counters of dsa_attn_fwd (for any call of a head
+ *                         count / for one call shape).
  */
 #ifndef DSA_ABI_H
 #define DSA_ABI_H
@@ -120,8 +122,13 @@ int dsa_attn_fwd(const dsa_attn_args *args, void *stream);
  * split_counters must be NULL: a split call keeps its fp32 partials in a
  * device array of DSA_NOALLOC_SCRATCH_BYTES that the library owns (one per
  * device, held until the process ends) and merges them with the separate
- * merge kernel.  Calls whose split workspace (dsa_attn_workspace_bytes) is
- * larger fail with DSA_EWORKSPACE.  The call allocates and frees nothing.
+ * merge kernel.  With num_splits = 0 the call takes the automatic split count
+ * or, when that count's workspace (dsa_attn_workspace_bytes) is larger than
+ * the array, the most splits below it whose workspace fits (one split needs
+ * none); an explicit num_splits whose workspace is larger fails with
+ * DSA_EWORKSPACE.  The call allocates and frees nothing.  Its first call on
+ * a device looks up the array's address (with the calling thread's stream
+ * capture mode relaxed for that lookup, so it may run under graph capture).
  * Calls that overlap on one device share the array and race.
  */
 #define DSA_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
@@ -140,6 +147,15 @@ size_t dsa_attn_workspace_bytes(int64_t num_tokens, int64_t num_heads, int64_t t
  * heads (any top-k and split count); 0 when calls with this head count always
  * merge with the separate kernel. */
 size_t dsa_attn_counter_bytes(int64_t num_tokens, int64_t num_heads);
+
+/* Split counters one call of this shape actually uses (requested_splits as in
+ * dsa_attn_args.num_splits): dsa_attn_counter_bytes(num_tokens, num_heads)
+ * when the call merges its splits inside the attention kernel (2 to 4
+ * splits, an odd number of 16-head groups), else 0 -- the call then runs the
+ * separate merge kernel and never touches counters.  No counterpart in the
+ * reference. */
+size_t dsa_attn_call_counter_bytes(int64_t num_tokens, int64_t num_heads, int64_t topk,
+                                   int32_t requested_splits);
 
 /*
  * The two halves of a split dsa_attn_fwd, for callers that merge partials

@@ -46,12 +46,33 @@ def oracle_mod():
     return oracle
 
 
+LDS_POISON_LIB = os.path.join(os.path.dirname(os.path.abspath(__file__)), "liblds_poison.so")
+# NaN as fp32 and as each of its bf16 halves; a negative int32
+LDS_POISON_PATTERN = 0xFFC0FFC0
+_poison = None
+
+
 def fill_lds_with_nan(device):
-    """Leaves NaN bit patterns in the LDS of every CU: a bf16 GEMM of NaN
-    operands (4096^3, more than one workgroup per CU) stages its tiles there,
-    and LDS is not cleared between workgroups.  A kernel launched next on the
-    same stream that reads an LDS location before writing it then computes
-    with NaN, which the parity checks see."""
+    """Leaves a NaN bit pattern in the whole LDS of every CU: 4096 workgroups
+    of the test-support kernel in tests/lds_poison.hip (built by
+    ``__graft_entry__.build()``), each taking all 160 KB of a CU's LDS and
+    writing the pattern over it.  LDS is not cleared between workgroups, so a
+    kernel launched next on the same stream that reads an LDS location before
+    writing it computes with NaN (or a negative slot id), which the parity
+    checks see."""
+    import ctypes
+
     import torch
-    a = torch.full((4096, 4096), float("nan"), dtype=torch.bfloat16, device=device)
-    return a @ a
+    global _poison
+    if _poison is None:
+        if not os.path.exists(LDS_POISON_LIB):
+            raise RuntimeError(f"{LDS_POISON_LIB} is missing: run __graft_entry__.build() first")
+        lib = ctypes.CDLL(LDS_POISON_LIB)
+        lib.lds_poison_fill.argtypes = [ctypes.c_uint32, ctypes.c_int, ctypes.c_void_p]
+        lib.lds_poison_fill.restype = ctypes.c_int
+        _poison = lib
+    dev = torch.device(device)
+    stream = torch._C._cuda_getCurrentRawStream(dev.index if dev.index is not None else 0)
+    rc = _poison.lds_poison_fill(LDS_POISON_PATTERN, 4096, stream)
+    if rc != 0:
+        raise RuntimeError(f"lds_poison_fill failed with HIP status {rc}")

@@ -95,6 +95,17 @@ def test_split_choice():
     assert lib.dsa_attn_counter_bytes(256, 128) == 0
     assert lib.dsa_attn_counter_bytes(8, 32) == 0
     assert lib.dsa_attn_counter_bytes(0, 16) == 0
+    # per call: only calls that merge inside the kernel (2..4 splits, odd
+    # group counts) use counters
+    assert lib.dsa_attn_call_counter_bytes(64, 16, 2048, 0) == 64 * 8 * 4   # 4 splits
+    assert lib.dsa_attn_call_counter_bytes(64, 16, 2048, 2) == 64 * 8 * 4
+    assert lib.dsa_attn_call_counter_bytes(1, 16, 2048, 0) == 0             # 16 splits
+    assert lib.dsa_attn_call_counter_bytes(48, 16, 2048, 5) == 0
+    assert lib.dsa_attn_call_counter_bytes(64, 16, 2048, 1) == 0            # no split
+    assert lib.dsa_attn_call_counter_bytes(2048, 16, 2048, 0) == 0
+    assert lib.dsa_attn_call_counter_bytes(64, 128, 2048, 2) == 0           # even group count
+    assert lib.dsa_attn_call_counter_bytes(4, 48, 2048, 3) == 4 * 3 * 8 * 4
+    assert lib.dsa_attn_call_counter_bytes(4, 16, 2048, -1) == 0
 
 
 def _args(**kw):
