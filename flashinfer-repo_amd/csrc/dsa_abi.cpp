@@ -364,9 +364,10 @@ size_t up256(size_t x) { return (x + 255) / 256 * 256; }
 }  // namespace
 
 namespace dsa {
-IndexerWorkspace indexer_workspace_layout(int64_t T, int64_t Hi, int64_t S, bool own_scores) {
+IndexerWorkspace indexer_workspace_layout(int64_t T, int64_t Hi, int64_t S, bool own_scores,
+                                          bool own_k) {
   IndexerWorkspace w = {};
-  const size_t kblocks = (size_t)(S + 15) / 16, qblocks = (size_t)T * (size_t)(Hi / 16);
+  const size_t kblocks = own_k ? (size_t)(S + 15) / 16 : 0, qblocks = (size_t)T * (size_t)(Hi / 16);
   size_t off = 0;
   w.k_pieces = off;
   off += up256(kblocks * 3 * 2 * 1024);
@@ -377,11 +378,21 @@ IndexerWorkspace indexer_workspace_layout(int64_t T, int64_t Hi, int64_t S, bool
   w.q_max = off;
   off += up256(qblocks * 4);
   w.k_cs = off;
-  off += up256((size_t)S * 4);
+  if (own_k) off += up256((size_t)S * 4);
   w.scores = off;
   if (own_scores) off += up256((size_t)T * (size_t)S * 4);
   w.total = off;
   return w;
+}
+
+KPlanesLayout k_planes_layout(int64_t C) {
+  KPlanesLayout l = {};
+  const size_t kblocks = (size_t)(C + 15) / 16;
+  l.k_pieces = 0;
+  l.k_max = up256(kblocks * 3 * 2 * 1024);
+  l.k_cs = l.k_max + up256(kblocks * 4);
+  l.total = l.k_cs + up256((size_t)C * 4);
+  return l;
 }
 }  // namespace dsa
 
@@ -390,7 +401,18 @@ extern "C" {
 size_t dsa_indexer_workspace_bytes(int64_t num_tokens, int64_t num_heads, int64_t head_dim,
                                    int64_t num_positions) {
   if (num_tokens < 0 || num_heads < 0 || head_dim < 0 || num_positions < 0) return 0;
-  return dsa::indexer_workspace_layout(num_tokens, num_heads, num_positions, true).total;
+  return dsa::indexer_workspace_layout(num_tokens, num_heads, num_positions, true, true).total;
+}
+
+size_t dsa_indexer_workspace_bytes_prepared(int64_t num_tokens, int64_t num_heads,
+                                            int64_t head_dim, int64_t num_positions) {
+  if (num_tokens < 0 || num_heads < 0 || head_dim < 0 || num_positions < 0) return 0;
+  return dsa::indexer_workspace_layout(num_tokens, num_heads, num_positions, true, false).total;
+}
+
+size_t dsa_indexer_k_planes_bytes(int64_t capacity) {
+  if (capacity < 0 || capacity > 0x7fffffffLL) return 0;
+  return dsa::k_planes_layout(capacity).total;
 }
 
 int dsa_indexer_topk(const dsa_indexer_args *a, void *stream) {
@@ -407,7 +429,8 @@ int dsa_indexer_topk(const dsa_indexer_args *a, void *stream) {
       a->num_tokens * a->num_positions > (1LL << 40))
     return fail(DSA_EUNSUPPORTED, "%s: size beyond the supported range", fn);
   if (a->num_tokens == 0) return ok();
-  const bool paged = a->k_cache != nullptr;
+  const bool prepared = a->k_planes != nullptr;
+  const bool paged = !prepared && a->k_cache != nullptr;
   if (paged && (a->k_idx || a->k_scale))
     return fail(DSA_EINVAL, "%s: give k_idx/k_scale or k_cache, not both", fn);
   if (paged && (!a->k_pages || a->k_page_size <= 0 || a->k_page_size % 4 != 0 ||
@@ -415,7 +438,7 @@ int dsa_indexer_topk(const dsa_indexer_args *a, void *stream) {
     return fail(DSA_EINVAL, "%s: k_cache needs k_pages and a k_page_size that is a positive "
                 "multiple of 4 (got %lld)", fn, (long long)a->k_page_size);
   if (!a->q_idx || !a->weights || !a->causal_limit || (a->topk > 0 && !a->out) ||
-      (a->num_positions > 0 && !paged && (!a->k_idx || !a->k_scale)))
+      (a->num_positions > 0 && !paged && !prepared && (!a->k_idx || !a->k_scale)))
     return fail(DSA_EINVAL, "%s: NULL tensor pointer", fn);
   if (!aligned(a->q_idx, 16) || !aligned(a->k_idx, 16) || !aligned(a->k_scale, 4) ||
       !aligned(a->weights, 4) || !aligned(a->causal_limit, 4) || !aligned(a->out, 4) ||
@@ -435,8 +458,13 @@ int dsa_indexer_topk(const dsa_indexer_args *a, void *stream) {
   if (paged && (a->k_num_pages <= 0 || a->k_num_pages > 0x7fffffffLL))
     return fail(DSA_EINVAL, "%s: k_cache needs k_num_pages >= 1 (got %lld)", fn,
                 (long long)a->k_num_pages);
+  if (prepared && (a->k_planes_capacity < a->num_positions || a->k_planes_capacity > 0x7fffffffLL ||
+                   !aligned(a->k_planes, 256)))
+    return fail(DSA_EINVAL, "%s: k_planes must be 256-byte aligned and laid out for at least "
+                "num_positions = %lld positions (k_planes_capacity %lld)", fn,
+                (long long)a->num_positions, (long long)a->k_planes_capacity);
   const dsa::IndexerWorkspace lay = dsa::indexer_workspace_layout(
-      a->num_tokens, a->num_heads, a->num_positions, a->scores_out == nullptr);
+      a->num_tokens, a->num_heads, a->num_positions, a->scores_out == nullptr, !prepared);
   if (!a->workspace || a->workspace_bytes < lay.total || !aligned(a->workspace, 256))
     return fail(DSA_EWORKSPACE, "%s: workspace of %zu bytes (256-byte aligned) needed, got %zu",
                 fn, lay.total, a->workspace ? a->workspace_bytes : (size_t)0);
@@ -456,11 +484,24 @@ int dsa_indexer_topk(const dsa_indexer_args *a, void *stream) {
   p.page_size = (int32_t)(a->block_table ? a->page_size : 1);
   p.out = a->out;
   char *ws = static_cast<char *>(a->workspace);
-  p.k_pieces = reinterpret_cast<int8_t *>(ws + lay.k_pieces);
-  p.k_max = reinterpret_cast<int32_t *>(ws + lay.k_max);
   p.q_pieces = reinterpret_cast<int8_t *>(ws + lay.q_pieces);
   p.q_max = reinterpret_cast<int32_t *>(ws + lay.q_max);
-  p.k_cs = reinterpret_cast<float *>(ws + lay.k_cs);
+  if (prepared) {
+    const dsa::KPlanesLayout kl = dsa::k_planes_layout(a->k_planes_capacity);
+    char *kp = static_cast<char *>(const_cast<void *>(a->k_planes));
+    p.k_pieces = reinterpret_cast<int8_t *>(kp + kl.k_pieces);
+    p.k_max = reinterpret_cast<int32_t *>(kp + kl.k_max);
+    p.k_cs = reinterpret_cast<float *>(kp + kl.k_cs);
+    p.k = nullptr;
+    p.k_scale = nullptr;
+    p.k_block0 = p.k_blocks = 0;
+  } else {
+    p.k_pieces = reinterpret_cast<int8_t *>(ws + lay.k_pieces);
+    p.k_max = reinterpret_cast<int32_t *>(ws + lay.k_max);
+    p.k_cs = reinterpret_cast<float *>(ws + lay.k_cs);
+    p.k_block0 = 0;
+    p.k_blocks = (int32_t)((a->num_positions + 15) / 16);
+  }
   if (paged) {
     p.k_cache = a->k_cache;
     p.k_pages = a->k_pages;
@@ -469,6 +510,58 @@ int dsa_indexer_topk(const dsa_indexer_args *a, void *stream) {
   }
   p.scores = a->scores_out ? a->scores_out : reinterpret_cast<float *>(ws + lay.scores);
   const hipError_t e = dsa::launch_indexer(p, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(DSA_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
+  return ok();
+}
+
+int dsa_indexer_prepare_k(const dsa_indexer_k_prepare_args *a, void *stream) {
+  const char *fn = "dsa_indexer_prepare_k";
+  if (!a) return fail(DSA_EINVAL, "%s: args is NULL", fn);
+  if (a->num_positions < 0 || a->num_positions > 0x7fffffffLL || a->first_position < 0 ||
+      a->count < 0)
+    return fail(DSA_EINVAL, "%s: negative size or position", fn);
+  if (a->k_planes_capacity < a->num_positions || a->k_planes_capacity > 0x7fffffffLL)
+    return fail(DSA_EINVAL, "%s: k_planes_capacity %lld is below num_positions %lld", fn,
+                (long long)a->k_planes_capacity, (long long)a->num_positions);
+  if (a->first_position > a->num_positions || a->count > a->num_positions - a->first_position)
+    return fail(DSA_EINVAL, "%s: positions [%lld, %lld) lie outside the %lld positions", fn,
+                (long long)a->first_position, (long long)(a->first_position + a->count),
+                (long long)a->num_positions);
+  if (a->count == 0) return ok();
+  if (!a->k_planes || !aligned(a->k_planes, 256))
+    return fail(DSA_EINVAL, "%s: k_planes must be a 256-byte aligned buffer", fn);
+  const bool paged = a->k_cache != nullptr;
+  if (paged && (a->k_idx || a->k_scale))
+    return fail(DSA_EINVAL, "%s: give k_idx/k_scale or k_cache, not both", fn);
+  if (paged && (!a->k_pages || a->k_page_size <= 0 || a->k_page_size % 4 != 0 ||
+                a->k_page_size > (1 << 24) || a->k_num_pages <= 0 ||
+                a->k_num_pages > 0x7fffffffLL))
+    return fail(DSA_EINVAL, "%s: k_cache needs k_pages, a k_page_size that is a positive multiple "
+                "of 4 and k_num_pages >= 1", fn);
+  if (!paged && (!a->k_idx || !a->k_scale)) return fail(DSA_EINVAL, "%s: NULL tensor pointer", fn);
+  if (!aligned(a->k_idx, 16) || !aligned(a->k_scale, 4) || !aligned(a->k_cache, 16) ||
+      !aligned(a->k_pages, 4))
+    return fail(DSA_EINVAL, "%s: misaligned pointer (e4m3 rows need 16 bytes)", fn);
+  const dsa::KPlanesLayout kl = dsa::k_planes_layout(a->k_planes_capacity);
+  char *kp = static_cast<char *>(a->k_planes);
+  dsa::IndexerParams p = {};
+  p.k = a->k_idx;
+  p.k_scale = a->k_scale;
+  if (paged) {
+    p.k_cache = a->k_cache;
+    p.k_pages = a->k_pages;
+    p.k_page_size = (int32_t)a->k_page_size;
+    p.k_num_pages = (int32_t)a->k_num_pages;
+  }
+  p.S = (int32_t)a->num_positions;
+  p.Hi = 16;
+  p.k_pieces = reinterpret_cast<int8_t *>(kp + kl.k_pieces);
+  p.k_max = reinterpret_cast<int32_t *>(kp + kl.k_max);
+  p.k_cs = reinterpret_cast<float *>(kp + kl.k_cs);
+  const int64_t b0 = a->first_position / 16, b1 = (a->first_position + a->count + 15) / 16;
+  p.k_block0 = (int32_t)b0;
+  p.k_blocks = (int32_t)(b1 - b0);
+  const hipError_t e = dsa::launch_indexer_prepare_k(p, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(DSA_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
   return ok();
 }

@@ -123,9 +123,10 @@ __device__ __forceinline__ i32x4 mfma(i32x4 a, i32x4 b, i32x4 c) {
 
 // ---- operand preparation -------------------------------------------------
 //
-// Destination blocks 0 .. ceil(S/16)-1 are k blocks (16 positions); the
-// following T*Hi/16 are q head blocks (token t, head block hb).  One wave
-// prepares one destination block; lane l = 16*g + c loads the 2 x 16 bytes it
+// Destination blocks 0 .. k_blocks-1 are k blocks k_block0 .. (16 positions
+// each; none when the call uses prepared K planes); the following T*Hi/16 are
+// q head blocks (token t, head block hb).  One wave prepares one destination
+// block; lane l = 16*g + c loads the 2 x 16 bytes it
 // writes: row c at dims 64*ks + 16*g for k-steps ks = 0, 1, so every plane
 // store of the wave is one contiguous 1 KB operand chunk.
 //
@@ -147,11 +148,12 @@ __global__ __launch_bounds__(kPrepThreads) void dsa_idx_prep_kernel(IndexerParam
   __syncthreads();
   const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nkb = (p.S + 15) >> 4, nqb = p.Hi >> 4;
-  const int total = nkb + p.T * nqb;
-  const int blk = blockIdx.x * (kPrepThreads / 64) + wave;
-  if (blk >= total) return;
-  const bool is_k = blk < nkb;
+  const int nqb = p.Hi >> 4;
+  const int total = p.k_blocks + p.T * nqb;
+  const int wblk = blockIdx.x * (kPrepThreads / 64) + wave;
+  if (wblk >= total) return;
+  const bool is_k = wblk < p.k_blocks;
+  const int blk = is_k ? p.k_block0 + wblk : wblk;  // k block index, or k_blocks + q block
 
   uint4 raw[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
   int8_t *dst;
@@ -177,7 +179,7 @@ __global__ __launch_bounds__(kPrepThreads) void dsa_idx_prep_kernel(IndexerParam
     }
     dst = p.k_pieces + (int64_t)blk * kBlockBytes + lane * 16;
   } else {
-    const int qb = blk - nkb, t = qb / nqb, hb = qb % nqb;
+    const int qb = wblk - p.k_blocks, t = qb / nqb, hb = qb % nqb;
     const int head = (c >> 2) * (p.Hi >> 2) + 4 * hb + (c & 3);
     const uint8_t *row = p.q + ((int64_t)t * p.Hi + head) * kIdxDim;
     raw[0] = *(const uint4 *)(row + g * 16);
@@ -197,7 +199,7 @@ __global__ __launch_bounds__(kPrepThreads) void dsa_idx_prep_kernel(IndexerParam
   const bool two = bmax < kTwoPieceLimit;
   if (lane == 0) {
     if (is_k) p.k_max[blk] = bmax;
-    else p.q_max[blk - nkb] = bmax;
+    else p.q_max[wblk - p.k_blocks] = bmax;
   }
 
   uint32_t v[32];
@@ -1168,11 +1170,22 @@ hipError_t launch_k_append(const KAppendParams &p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+hipError_t launch_indexer_prepare_k(const IndexerParams &pin, hipStream_t stream) {
+  IndexerParams p = pin;
+  p.T = 0;  // k blocks only
+  if (p.k_blocks <= 0) return hipSuccess;
+  const int prep_blocks = (p.k_blocks + kPrepThreads / 64 - 1) / (kPrepThreads / 64);
+  hipLaunchKernelGGL(dsa_idx_prep_kernel, dim3(prep_blocks), dim3(kPrepThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
 hipError_t launch_indexer(const IndexerParams &pin, hipStream_t stream) {
   if (pin.T == 0) return hipSuccess;
   IndexerParams p = pin;
   const int nkb = (p.S + 15) / 16, nqb = p.Hi / 16;
-  const int prep_blocks = (nkb + p.T * nqb + kPrepThreads / 64 - 1) / (kPrepThreads / 64);
+  // k blocks [k_block0, k_block0 + k_blocks) are prepared with the q blocks
+  // (none when the caller's prepared K planes are used)
+  const int prep_blocks = (p.k_blocks + p.T * nqb + kPrepThreads / 64 - 1) / (kPrepThreads / 64);
   hipLaunchKernelGGL(dsa_idx_prep_kernel, dim3(prep_blocks), dim3(kPrepThreads), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;

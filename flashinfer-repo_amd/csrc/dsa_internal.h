@@ -139,6 +139,9 @@ struct IndexerParams {
   int8_t *q_pieces;
   int32_t *q_max;
   int32_t blocks_per_wg;  // 16-position blocks one score workgroup walks (set by the launcher)
+  // k blocks the prep kernel derives planes for: [k_block0, k_block0 + k_blocks)
+  // (0 blocks when the call reads prepared K planes)
+  int32_t k_block0, k_blocks;
 };
 
 struct IndexerWorkspace {
@@ -146,10 +149,21 @@ struct IndexerWorkspace {
 };
 
 // Offsets of the indexer's workspace regions; scores are left out when the
-// caller provides the score buffer.
-IndexerWorkspace indexer_workspace_layout(int64_t T, int64_t Hi, int64_t S, bool own_scores);
+// caller provides the score buffer, the k regions when the call reads
+// prepared K planes.
+IndexerWorkspace indexer_workspace_layout(int64_t T, int64_t Hi, int64_t S, bool own_scores,
+                                          bool own_k);
 
 hipError_t launch_indexer(const IndexerParams &p, hipStream_t stream);
+// Only the k planes of blocks [k_block0, k_block0 + k_blocks) (K preparation).
+hipError_t launch_indexer_prepare_k(const IndexerParams &p, hipStream_t stream);
+
+// Prepared K planes (dsa_indexer_prepare_k): the K half of the workspace
+// layout, [k_pieces][k_max][k_cs] of S positions, 256-byte aligned regions.
+struct KPlanesLayout {
+  size_t k_pieces, k_max, k_cs, total;
+};
+KPlanesLayout k_planes_layout(int64_t S);
 
 // Quantise-on-append into the paged indexer K cache (layout above).
 struct KAppendParams {

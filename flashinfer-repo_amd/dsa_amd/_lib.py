@@ -19,7 +19,7 @@ DSA_EINVAL = 1
 DSA_EUNSUPPORTED = 2
 DSA_ELAUNCH = 3
 DSA_EWORKSPACE = 4
-ABI_VERSION = 4
+ABI_VERSION = 5
 NOALLOC_SCRATCH_BYTES = 32 << 20   # DSA_NOALLOC_SCRATCH_BYTES
 
 EXPORTED_SYMBOLS = (
@@ -35,6 +35,9 @@ EXPORTED_SYMBOLS = (
     "dsa_indexer_topk",
     "dsa_indexer_k_append",
     "dsa_indexer_workspace_bytes",
+    "dsa_indexer_workspace_bytes_prepared",
+    "dsa_indexer_k_planes_bytes",
+    "dsa_indexer_prepare_k",
     "dsa_last_error",
     "dsa_abi_version",
 )
@@ -88,6 +91,18 @@ class IndexerArgs(ctypes.Structure):
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
         ("k_cache", _vp), ("k_pages", _vp), ("k_page_size", _i64),
         ("block_table_width", _i64), ("k_num_pages", _i64),
+        ("k_planes", _vp), ("k_planes_capacity", _i64),
+    ]
+
+
+class KPrepareArgs(ctypes.Structure):
+    """Mirror of ``dsa_indexer_k_prepare_args``."""
+
+    _fields_ = [
+        ("k_idx", _vp), ("k_scale", _vp), ("k_cache", _vp), ("k_pages", _vp),
+        ("k_page_size", _i64), ("k_num_pages", _i64), ("num_positions", _i64),
+        ("first_position", _i64), ("count", _i64),
+        ("k_planes", _vp), ("k_planes_capacity", _i64),
     ]
 
 
@@ -149,6 +164,12 @@ def load() -> ctypes.CDLL:
     lib.dsa_indexer_k_append.restype = ctypes.c_int
     lib.dsa_indexer_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64]
     lib.dsa_indexer_workspace_bytes.restype = ctypes.c_size_t
+    lib.dsa_indexer_workspace_bytes_prepared.argtypes = [_i64, _i64, _i64, _i64]
+    lib.dsa_indexer_workspace_bytes_prepared.restype = ctypes.c_size_t
+    lib.dsa_indexer_k_planes_bytes.argtypes = [_i64]
+    lib.dsa_indexer_k_planes_bytes.restype = ctypes.c_size_t
+    lib.dsa_indexer_prepare_k.argtypes = [ctypes.POINTER(KPrepareArgs), _vp]
+    lib.dsa_indexer_prepare_k.restype = ctypes.c_int
     lib.dsa_last_error.argtypes = []
     lib.dsa_last_error.restype = ctypes.c_char_p
     lib.dsa_abi_version.argtypes = []

@@ -87,12 +87,18 @@ def run_indexer_and_topk(*args, **kwargs):
     ``block_table[page] * page_size + offset``.  With ``return_scores`` the
     fp32 ``[T, S]`` scores (masked entries -inf) are returned too.
 
+    With ``k_planes`` (a :class:`KPlanes` from :func:`prepare_k` or
+    :func:`prepare_k_paged`) the call reads the prepared K operand planes
+    instead of deriving them from ``k_idx``/``k_scale`` (which may then be
+    None; the sequence length is the planes' ``num_positions``); the results
+    are the same bits.
+
     Calls with the reference's per-sequence argument list
     (``indexer_kernel.py:345-363``) raise ``TypeError`` naming the layout
     difference.
     """
     names = ("q_idx", "k_idx", "k_scale", "weights", "causal_limit", "topk", "block_table",
-             "page_size", "return_scores")
+             "page_size", "return_scores", "k_planes")
     mine = {k: kwargs.pop(k) for k in names if k in kwargs}
     _reject_reference_layout("run_indexer_and_topk", "indexer_kernel.py:345-363", len(args),
                              len(names), kwargs)
@@ -107,10 +113,19 @@ def run_indexer_and_topk(*args, **kwargs):
     return _run_indexer_and_topk(**bound)
 
 
-def _run_indexer_and_topk(q_idx: torch.Tensor, k_idx: torch.Tensor, k_scale: torch.Tensor,
-                          weights: torch.Tensor, causal_limit: torch.Tensor, topk: int,
+def _run_indexer_and_topk(q_idx: torch.Tensor, k_idx: Optional[torch.Tensor],
+                          k_scale: Optional[torch.Tensor], weights: torch.Tensor,
+                          causal_limit: torch.Tensor, topk: int,
                           block_table: Optional[torch.Tensor] = None, page_size: int = 64,
-                          return_scores: bool = False):
+                          return_scores: bool = False, k_planes: Optional["KPlanes"] = None):
+    if k_planes is not None:
+        _check(isinstance(k_planes, KPlanes), "k_planes must be a KPlanes (see prepare_k)")
+        S = k_planes.num_positions
+        if k_idx is not None:
+            _check(k_idx.shape[0] == S, f"k_idx holds {k_idx.shape[0]} positions, the planes {S}")
+        return _indexer(q_idx, S, weights, causal_limit, topk, block_table, page_size,
+                        return_scores, planes=k_planes)
+    _check(k_idx is not None and k_scale is not None, "k_idx and k_scale are required without k_planes")
     k = _codes(k_idx, "k_idx")
     _check(k.dim() == 2 and k.shape[1] == INDEX_HEAD_DIM,
            f"k_idx must be [S, {INDEX_HEAD_DIM}], got {tuple(k.shape)}")
@@ -142,7 +157,7 @@ def run_indexer_and_topk_paged(q_idx: torch.Tensor, k_cache: torch.Tensor, k_pag
 
 
 def _indexer(q_idx, S, weights, causal_limit, topk, block_table, page_size, return_scores,
-             flat=None, paged=None):
+             flat=None, paged=None, planes=None):
     q = _codes(q_idx, "q_idx")
     _check(q.dim() == 3 and q.shape[2] == INDEX_HEAD_DIM,
            f"q_idx must be [T, heads, {INDEX_HEAD_DIM}], got {tuple(q.shape)}")
@@ -155,7 +170,7 @@ def _indexer(q_idx, S, weights, causal_limit, topk, block_table, page_size, retu
     _check(tuple(w.shape) == (T, Hi) and w.dtype == torch.float32, "weights must be [T, heads] float32")
     _check(tuple(lim.shape) == (T,) and lim.dtype == torch.int32, "causal_limit must be [T] int32")
     _check(int(topk) >= 0, "topk must be >= 0")
-    held = [x for x in (flat or paged) if isinstance(x, torch.Tensor)]
+    held = [x for x in (flat or paged or (planes.buf,)) if isinstance(x, torch.Tensor)]
     for name, x in [("weights", w), ("causal_limit", lim)] + [("k", x) for x in held]:
         _check(x.device == dev, f"{name} is on {x.device}, expected {dev}")
     bt = None
@@ -177,11 +192,16 @@ def _indexer(q_idx, S, weights, causal_limit, topk, block_table, page_size, retu
     lib = _lib.load()
     out = torch.empty((T, int(topk)), dtype=torch.int32, device=dev)
     scores = torch.empty((T, S), dtype=torch.float32, device=dev) if return_scores else None
-    ws_bytes = lib.dsa_indexer_workspace_bytes(T, Hi, INDEX_HEAD_DIM, S)
+    if planes is not None:
+        ws_bytes = lib.dsa_indexer_workspace_bytes_prepared(T, Hi, INDEX_HEAD_DIM, S)
+    else:
+        ws_bytes = lib.dsa_indexer_workspace_bytes(T, Hi, INDEX_HEAD_DIM, S)
     ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
     a = _lib.IndexerArgs()
     a.q_idx, a.weights = q.data_ptr(), w.data_ptr()
-    if flat is not None:
+    if planes is not None:
+        a.k_planes, a.k_planes_capacity = planes.buf.data_ptr(), planes.capacity
+    elif flat is not None:
         a.k_idx, a.k_scale = flat[0].data_ptr(), flat[1].data_ptr()
     else:
         a.k_cache, a.k_pages, a.k_page_size = paged[0].data_ptr(), paged[1].data_ptr(), paged[2]
@@ -196,6 +216,91 @@ def _indexer(q_idx, S, weights, causal_limit, topk, block_table, page_size, retu
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
     _lib.check("dsa_indexer_topk", lib.dsa_indexer_topk(ctypes.byref(a), _stream_handle(dev)))
     return (out, scores) if return_scores else out
+
+
+class KPlanes:
+    """MFMA operand planes of an indexer K sequence, kept beside the K cache
+    (``dsa_indexer_prepare_k``): per 16-position block the e4m3 values as
+    signed 7-bit pieces in MFMA lane order and the block's largest magnitude,
+    and ``fl32(k_scale * 2^-18)`` per position, for up to ``capacity``
+    positions.  ``num_positions`` is the sequence length the planes were last
+    prepared for.  Made by :func:`prepare_k` / :func:`prepare_k_paged`, which
+    also refresh positions of an existing object after an append; pass it to
+    :func:`run_indexer_and_topk` as ``k_planes``."""
+
+    def __init__(self, capacity: int, device):
+        _check(int(capacity) >= 0, "capacity must be >= 0")
+        self.capacity = int(capacity)
+        nbytes = _lib.load().dsa_indexer_k_planes_bytes(self.capacity)
+        # 256-byte aligned: the caching allocator's blocks start at 512-byte boundaries
+        self.buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _check(self.buf.data_ptr() % 256 == 0, "planes buffer is not 256-byte aligned")
+        self.num_positions = 0
+
+
+def _planes_for(planes, S, capacity, dev):
+    if planes is None:
+        planes = KPlanes(S if capacity is None else capacity, dev)
+    _check(isinstance(planes, KPlanes), "planes must be a KPlanes")
+    _check(planes.capacity >= S, f"the planes hold {planes.capacity} positions, {S} needed")
+    _check(planes.buf.device == dev, f"planes are on {planes.buf.device}, expected {dev}")
+    return planes
+
+
+def _prepare(a, planes, S, first_position, count):
+    first = int(first_position)
+    n = S - first if count is None else int(count)
+    a.num_positions, a.first_position, a.count = S, first, n
+    a.k_planes, a.k_planes_capacity = planes.buf.data_ptr(), planes.capacity
+    lib = _lib.load()
+    _lib.check("dsa_indexer_prepare_k",
+               lib.dsa_indexer_prepare_k(ctypes.byref(a), _stream_handle(planes.buf.device)))
+    planes.num_positions = S
+    return planes
+
+
+def prepare_k(k_idx: torch.Tensor, k_scale: torch.Tensor, planes: Optional[KPlanes] = None,
+              first_position: int = 0, count: Optional[int] = None,
+              capacity: Optional[int] = None) -> KPlanes:
+    """Derive the K operand planes of ``k_idx [S, 128]`` e4m3fn with
+    ``k_scale [S]`` fp32 for positions ``[first_position, first_position +
+    count)`` (default: all) -- into ``planes`` when given (e.g. after
+    appending positions), else into new planes of ``capacity`` (default S)
+    positions.  Returns the planes, now describing S positions."""
+    k = _codes(k_idx, "k_idx")
+    _check(k.dim() == 2 and k.shape[1] == INDEX_HEAD_DIM,
+           f"k_idx must be [S, {INDEX_HEAD_DIM}], got {tuple(k.shape)}")
+    S = k.shape[0]
+    sc = k_scale.contiguous()
+    _check(tuple(sc.shape) == (S,) and sc.dtype == torch.float32, "k_scale must be [S] float32")
+    _check(k.device.type == "cuda" and sc.device == k.device, "k_idx and k_scale must be on one GPU")
+    planes = _planes_for(planes, S, capacity, k.device)
+    a = _lib.KPrepareArgs()
+    a.k_idx, a.k_scale = k.data_ptr(), sc.data_ptr()
+    return _prepare(a, planes, S, first_position, count)
+
+
+def prepare_k_paged(k_cache: torch.Tensor, k_pages: torch.Tensor, num_positions: int,
+                    planes: Optional[KPlanes] = None, first_position: int = 0,
+                    count: Optional[int] = None, capacity: Optional[int] = None) -> KPlanes:
+    """:func:`prepare_k` over a paged fp8 K cache (the format :func:`k_append`
+    writes), position ``s`` being token ``s % kps`` of page ``k_pages[s //
+    kps]``: after ``k_append`` of new positions, ``prepare_k_paged(cache,
+    pages, new_length, planes, first_position=old_length)`` refreshes only
+    the blocks the append touched."""
+    cache, kps = _k_cache_view(k_cache)
+    pages = k_pages.contiguous()
+    S = int(num_positions)
+    _check(S >= 0, "num_positions must be >= 0")
+    _check(pages.dtype == torch.int32 and pages.dim() == 1 and pages.numel() * kps >= S,
+           f"k_pages must be int32 [>= {-(-S // kps)}]")
+    _check(pages.device == cache.device and cache.device.type == "cuda",
+           "k_cache and k_pages must be on one GPU")
+    planes = _planes_for(planes, S, capacity, cache.device)
+    a = _lib.KPrepareArgs()
+    a.k_cache, a.k_pages, a.k_page_size = cache.data_ptr(), pages.data_ptr(), kps
+    a.k_num_pages = cache.shape[0]
+    return _prepare(a, planes, S, first_position, count)
 
 
 K_TOKEN_BYTES = INDEX_HEAD_DIM + 4  # e4m3 codes + fp32 scale per token
@@ -243,7 +348,7 @@ def k_append(k: torch.Tensor, slots: torch.Tensor, k_cache: torch.Tensor) -> tor
 
 _PIPELINE_ARGS = ("q_idx", "k_idx", "k_scale", "weights", "causal_limit", "block_table",
                   "q_nope", "q_pe", "ckv_cache", "kpe_cache", "sm_scale", "topk", "page_size",
-                  "k_cache", "k_pages", "num_positions")
+                  "k_cache", "k_pages", "num_positions", "k_planes")
 
 
 def run_sparse_attention_pipeline(*args, **kwargs):
@@ -256,7 +361,8 @@ def run_sparse_attention_pipeline(*args, **kwargs):
     num_positions=None)``.  ``page_size`` defaults to the cache's.
     With ``k_cache`` (a paged fp8 K cache, see :func:`k_append`; ``k_idx`` and
     ``k_scale`` then None) the indexer reads ``num_positions`` positions
-    through ``k_pages``, by default the sequence's 1-D ``block_table``.
+    through ``k_pages``, by default the sequence's 1-D ``block_table``; with
+    ``k_planes`` (see :func:`prepare_k`) it reads prepared K planes instead.
     Returns ``(output [T,H,512] bf16, lse [T,H] fp32 base-2, slots [T,topk])``.
     Calls with the reference's per-sequence argument list (``kernel.py:184-211``)
     raise ``TypeError`` naming the layout difference."""
@@ -278,9 +384,12 @@ def run_sparse_attention_pipeline(*args, **kwargs):
 def _pipeline(q_idx, k_idx, k_scale, weights, causal_limit, block_table, q_nope, q_pe, ckv_cache,
               kpe_cache, sm_scale, topk: int = 2048, page_size: Optional[int] = None,
               k_cache: Optional[torch.Tensor] = None, k_pages: Optional[torch.Tensor] = None,
-              num_positions: Optional[int] = None):
+              num_positions: Optional[int] = None, k_planes: Optional[KPlanes] = None):
     ps = int(page_size) if page_size is not None else (ckv_cache.shape[1] if ckv_cache.dim() == 3 else 1)
-    if k_cache is not None:
+    if k_planes is not None:
+        slots = _run_indexer_and_topk(q_idx, k_idx, k_scale, weights, causal_limit, topk,
+                                      block_table=block_table, page_size=ps, k_planes=k_planes)
+    elif k_cache is not None:
         _check(k_idx is None and k_scale is None, "give k_idx/k_scale or k_cache, not both")
         pages = k_pages if k_pages is not None else block_table
         _check(pages is not None and pages.dim() == 1,

@@ -26,6 +26,11 @@
  *   dsa_indexer_k_append  no kernel in the reference: writes the paged fp8
  *                         indexer K cache that indexer_kernel.py:163-197
  *                         reads (quantise-on-append).
+ *   dsa_indexer_prepare_k / dsa_indexer_k_planes_bytes /
+ *   dsa_indexer_workspace_bytes_prepared
+ *                         no counterpart: K operand planes kept beside the K
+ *                         cache, so a call skips the per-call re-read of K
+ *                         that indexer_kernel.py:185-275 does.
  *   dsa_attn_counter_bytes / dsa_attn_call_counter_bytes
  *                         no counterpart: size of the optional split
  *                         counters of dsa_attn_fwd (for any call of a head
@@ -41,7 +46,7 @@
 extern "C" {
 #endif
 
-#define DSA_ABI_VERSION 4
+#define DSA_ABI_VERSION 5
 
 #define DSA_OK 0
 #define DSA_EINVAL 1      /* bad pointer, size, stride or alignment */
@@ -252,9 +257,50 @@ typedef struct dsa_indexer_args {
    * k_pages entry lies outside [0, k_num_pages) reads as a zero row with a
    * zero scale (its score is 0); nothing outside k_cache is read. */
   int64_t k_num_pages;
+  /* Optional prepared K planes (ABI version 5; no counterpart in the
+   * reference): a buffer that dsa_indexer_prepare_k filled for at least these
+   * num_positions positions, laid out for k_planes_capacity >= num_positions
+   * positions (256-byte aligned, dsa_indexer_k_planes_bytes(capacity) bytes).
+   * The call then reads the K operands from it and does no K preparation;
+   * k_idx, k_scale and k_cache are ignored and may be NULL, and the workspace
+   * needs only dsa_indexer_workspace_bytes_prepared() bytes. */
+  const void *k_planes;
+  int64_t k_planes_capacity;
 } dsa_indexer_args;
 
 int dsa_indexer_topk(const dsa_indexer_args *args, void *stream);
+
+/*
+ * Prepared K planes (no counterpart in the reference, whose score kernel
+ * re-reads and dequantises K on every call, indexer_kernel.py:185-275).  The
+ * K cache changes only where tokens are appended, so the MFMA operand planes
+ * the score kernel reads (per 16-position block: the e4m3 values as signed
+ * 7-bit pieces in MFMA lane order, the block's largest magnitude, and
+ * fl32(k_scale * 2^-18) per position) can be derived once and kept beside
+ * the cache.  dsa_indexer_prepare_k (re)derives the blocks that hold
+ * positions [first_position, first_position + count) of a sequence of
+ * num_positions positions (flat k_idx/k_scale, or a paged K cache read
+ * through k_pages as in dsa_indexer_args; a block's positions at or past
+ * num_positions read as zeros), into a planes buffer laid out for
+ * k_planes_capacity positions.  After an append, re-preparing the appended
+ * positions keeps the planes current; calls of dsa_indexer_topk with those
+ * planes give the same bits as calls that prepare K themselves.
+ */
+typedef struct dsa_indexer_k_prepare_args {
+  const uint8_t *k_idx;     /* [num_positions, 128] e4m3fn codes, or NULL (paged) */
+  const float *k_scale;     /* [num_positions] */
+  const uint8_t *k_cache;   /* paged cache (then k_idx, k_scale NULL) */
+  const int32_t *k_pages;
+  int64_t k_page_size, k_num_pages;
+  int64_t num_positions;
+  int64_t first_position, count;
+  void *k_planes;           /* 256-byte aligned */
+  int64_t k_planes_capacity;
+} dsa_indexer_k_prepare_args;
+
+size_t dsa_indexer_k_planes_bytes(int64_t capacity);
+
+int dsa_indexer_prepare_k(const dsa_indexer_k_prepare_args *args, void *stream);
 
 /*
  * Paged fp8 indexer K cache and its quantise-on-append (the K-cache format on
@@ -289,6 +335,11 @@ int dsa_indexer_k_append(const dsa_k_append_args *args, void *stream);
 
 size_t dsa_indexer_workspace_bytes(int64_t num_tokens, int64_t num_heads, int64_t head_dim,
                                    int64_t num_positions);
+
+/* Workspace of a dsa_indexer_topk call that reads prepared K planes (the q
+ * operand pieces and, unless scores_out is given, the scores). */
+size_t dsa_indexer_workspace_bytes_prepared(int64_t num_tokens, int64_t num_heads,
+                                            int64_t head_dim, int64_t num_positions);
 
 /* Thread-local description of the last failure ("" if none). */
 const char *dsa_last_error(void);

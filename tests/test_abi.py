@@ -37,10 +37,11 @@ def test_header_functions_are_exported():
 def test_abi_version_and_struct_layout(tmp_path):
     """The ctypes mirrors match the C structs field by field (gcc offsetof)."""
     lib = _lib.load()
-    assert lib.dsa_abi_version() == _lib.ABI_VERSION == 4
+    assert lib.dsa_abi_version() == _lib.ABI_VERSION == 5
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "dsa_abi.h"', 'int main(void){']
     for cname, cls in (("dsa_attn_args", _lib.AttnArgs), ("dsa_indexer_args", _lib.IndexerArgs),
-                        ("dsa_k_append_args", _lib.KAppendArgs)):
+                        ("dsa_k_append_args", _lib.KAppendArgs),
+                        ("dsa_indexer_k_prepare_args", _lib.KPrepareArgs)):
         lines.append(f'printf("{cname} %zu\\n", sizeof({cname}));')
         for f, _ in cls._fields_:
             lines.append(f'printf("{cname}.{f} %zu\\n", offsetof({cname}, {f}));')
@@ -51,7 +52,8 @@ def test_abi_version_and_struct_layout(tmp_path):
     subprocess.check_call(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)])
     got = dict(l.split() for l in subprocess.check_output([str(exe)], text=True).splitlines())
     for cname, cls in (("dsa_attn_args", _lib.AttnArgs), ("dsa_indexer_args", _lib.IndexerArgs),
-                        ("dsa_k_append_args", _lib.KAppendArgs)):
+                        ("dsa_k_append_args", _lib.KAppendArgs),
+                        ("dsa_indexer_k_prepare_args", _lib.KPrepareArgs)):
         assert int(got[cname]) == ctypes.sizeof(cls)
         for f, _ in cls._fields_:
             assert int(got[f"{cname}.{f}"]) == getattr(cls, f).offset, f
@@ -253,6 +255,71 @@ def test_indexer_workspace_and_empty_call():
     want = up(kb * 6144) + up(kb * 4) + up(qb * 8192) + up(qb * 4) + up(1000 * 4) + up(3 * 1000 * 4)
     assert lib.dsa_indexer_workspace_bytes(3, 48, 128, 1000) == want
     assert lib.dsa_indexer_topk(ctypes.byref(_idx_args(num_tokens=0, q_idx=None)), None) == 0
+
+
+def test_k_planes_sizes():
+    """Prepared K planes hold exactly the K regions of a call's workspace: the
+    k operand chunks, the block maxima and the per-position scales."""
+    lib = _lib.load()
+
+    def up(x):
+        return (x + 255) // 256 * 256
+
+    for S in (32768, 1000, 1, 0):
+        kb = (S + 15) // 16
+        assert lib.dsa_indexer_k_planes_bytes(S) == up(kb * 6144) + up(kb * 4) + up(S * 4)
+        for T, H in ((64, 64), (3, 48)):
+            full = lib.dsa_indexer_workspace_bytes(T, H, 128, S)
+            assert full - lib.dsa_indexer_workspace_bytes_prepared(T, H, 128, S) == \
+                lib.dsa_indexer_k_planes_bytes(S)
+    assert lib.dsa_indexer_k_planes_bytes(-1) == 0
+
+
+def _prep_args(**kw):
+    a = _lib.KPrepareArgs()
+    base = dict(k_idx=0x2000, k_scale=0x3000, num_positions=32768, first_position=0,
+                count=32768, k_planes=0x10000, k_planes_capacity=32768)
+    base.update(kw)
+    for k, v in base.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,needle", [
+    (dict(k_planes_capacity=1000), "capacity"),
+    (dict(first_position=32000, count=1000), "outside"),
+    (dict(count=-1), "negative"),
+    (dict(k_planes=0x10010), "256-byte"),
+    (dict(k_idx=None), "NULL"),
+    (dict(k_idx=0x2004), "aligned"),
+    (dict(k_cache=0x9000), "not both"),
+    (dict(k_idx=None, k_scale=None, k_cache=0x9000, k_pages=0xa000, k_page_size=6,
+          k_num_pages=4), "multiple of 4"),
+])
+def test_prepare_k_host_validation(kw, needle):
+    lib = _lib.load()
+    rc = lib.dsa_indexer_prepare_k(ctypes.byref(_prep_args(**kw)), None)
+    assert rc == _lib.DSA_EINVAL and needle in lib.dsa_last_error().decode()
+    # nothing to prepare: accepted without a launch
+    assert lib.dsa_indexer_prepare_k(ctypes.byref(_prep_args(first_position=100, count=0)),
+                                     None) == 0
+
+
+def test_indexer_with_planes_host_validation():
+    """Planes laid out for fewer positions than the call reads are refused; a
+    call with planes needs no K source and only the smaller workspace."""
+    lib = _lib.load()
+    small = lib.dsa_indexer_workspace_bytes_prepared(64, 64, 128, 32768)
+    a = _idx_args(k_idx=None, k_scale=None, k_planes=0x10000, k_planes_capacity=1000,
+                  workspace_bytes=small)
+    assert lib.dsa_indexer_topk(ctypes.byref(a), None) == _lib.DSA_EINVAL
+    assert b"k_planes" in lib.dsa_last_error()
+    a = _idx_args(k_idx=None, k_scale=None, k_planes=0x10000, k_planes_capacity=32768,
+                  workspace_bytes=small - 256)
+    assert lib.dsa_indexer_topk(ctypes.byref(a), None) == _lib.DSA_EWORKSPACE
+    a = _idx_args(k_idx=None, k_scale=None, k_planes=0x10080, k_planes_capacity=32768,
+                  workspace_bytes=small)
+    assert lib.dsa_indexer_topk(ctypes.byref(a), None) == _lib.DSA_EINVAL
 
 
 @pytest.mark.parametrize("kw,code,needle", [

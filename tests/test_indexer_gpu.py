@@ -15,7 +15,7 @@ import torch
 
 import oracle
 from conftest import LSE_ATOL, LSE_RTOL, OUT_ATOL, OUT_RTOL, fill_lds_with_nan, mismatches
-from dsa_amd import workloads
+from dsa_amd import _lib, workloads
 from dsa_amd.indexer_kernel import run_indexer_and_topk, run_sparse_attention_pipeline
 
 pytestmark = pytest.mark.gpu
@@ -412,3 +412,104 @@ def test_paged_indexer_unmapped_pages_read_as_zero_rows():
     assert np.array_equal(out.cpu().numpy(), ref_idx)
     ora_idx, ora_sc = _oracle(flat, topk)
     _assert_same(ref_idx, ref_sc, ora_idx, ora_sc, "flat with zeroed pages")
+
+
+# ---- prepared K planes ---------------------------------------------------
+
+def test_prepared_planes_give_the_same_bits():
+    """Calls reading planes from prepare_k (capacity above the sequence
+    length, the K tensors not passed) return the scores and sets of calls
+    that prepare K themselves, and those match the oracle; one planes object
+    serves several calls."""
+    from dsa_amd import prepare_k
+    d = workloads.cfg5()
+    g = workloads.to_device(d, DEV)
+    print("prepared planes cfg5", flush=True)
+    planes = prepare_k(g["k_idx"], g["k_scale"], capacity=40000)
+    assert planes.num_positions == d["k_idx"].shape[0]
+    args = (g["q_idx"], g["k_idx"], g["k_scale"], g["weights"], g["causal_limit"])
+    ref, ref_sc = run_indexer_and_topk(*args, 2048, return_scores=True)
+    for topk in (2048, 77):
+        out, sc = run_indexer_and_topk(g["q_idx"], None, None, g["weights"], g["causal_limit"],
+                                       topk, return_scores=True, k_planes=planes)
+        torch.cuda.synchronize()
+        assert torch.equal(sc.view(torch.int32), ref_sc.view(torch.int32))
+        if topk == 2048:
+            assert torch.equal(out, ref)
+    ora_idx, ora_sc = _oracle(d, 2048)
+    _assert_same(ref.cpu().numpy(), ref_sc.cpu().numpy(), ora_idx, ora_sc, "cfg5 with planes")
+    # the pipeline with planes gives the same slots, output and lse
+    a = (g["q_nope"], g["q_pe"], g["ckv_cache"], g["kpe_cache"], d["sm_scale"])
+    p1 = run_sparse_attention_pipeline(*args, g["block_table"], *a, topk=2048)
+    p2 = run_sparse_attention_pipeline(g["q_idx"], None, None, g["weights"], g["causal_limit"],
+                                       g["block_table"], *a, topk=2048, k_planes=planes)
+    torch.cuda.synchronize()
+    for x, y in zip(p1, p2):
+        assert torch.equal(x, y)
+
+
+def test_planes_refreshed_after_appends_match_a_full_preparation():
+    """A paged K cache grows by appends of uneven lengths (some ending inside
+    a 16-position block); after each append only the appended positions are
+    re-prepared.  The planes then equal a full preparation byte for byte and
+    the indexer over them equals the paged call without planes."""
+    from dsa_amd import KPlanes, k_append, new_k_cache, prepare_k_paged, run_indexer_and_topk_paged
+    gen = torch.Generator().manual_seed(61)
+    T, Hi, ps, topk = 8, 64, 64, 300
+    S_max = 3000
+    n_pages = -(-S_max // ps) + 2
+    page_of = torch.randperm(n_pages, generator=gen).to(torch.int32)
+    k = torch.randn(S_max, 128, generator=gen).to(torch.bfloat16)
+    pos = torch.arange(S_max)
+    slots = (page_of[pos // ps].long() * ps + pos % ps).to(torch.int32)
+    cache = new_k_cache(n_pages, ps, DEV)
+    pages = page_of.to(DEV)
+    planes = KPlanes(S_max, DEV)
+    S = 0
+    for n in (1000, 7, 9, 16, 1, 500, 1467):
+        k_append(k[S:S + n].to(DEV), slots[S:S + n].to(DEV), cache)
+        print(f"append {n} at {S}", flush=True)
+        prepare_k_paged(cache, pages, S + n, planes=planes, first_position=S)
+        S += n
+        full = prepare_k_paged(cache, pages, S, capacity=S_max)
+        torch.cuda.synchronize()
+        # blocks past S hold whatever earlier refreshes left; compare the
+        # regions the indexer reads for S positions
+        nkb = (S + 15) // 16
+        kpb = nkb * 6144
+        kmax_off = (((S_max + 15) // 16) * 6144 + 255) // 256 * 256
+        cs_off = kmax_off + ((((S_max + 15) // 16) * 4 + 255) // 256 * 256)
+        for lo, hi in ((0, kpb), (kmax_off, kmax_off + nkb * 4), (cs_off, cs_off + S * 4)):
+            assert torch.equal(planes.buf[lo:hi], full.buf[lo:hi]), (S, lo)
+        assert _lib.load().dsa_indexer_k_planes_bytes(S_max) == planes.buf.numel()
+        d = workloads.indexer_inputs(T=T, Hi=Hi, S=S, seed=62 + S)
+        gd = workloads.to_device(d, DEV)
+        ref, ref_sc = run_indexer_and_topk_paged(gd["q_idx"], cache, pages, S, gd["weights"],
+                                                 gd["causal_limit"], topk, return_scores=True)
+        out, sc = run_indexer_and_topk(gd["q_idx"], None, None, gd["weights"], gd["causal_limit"],
+                                       topk, return_scores=True, k_planes=planes)
+        torch.cuda.synchronize()
+        assert torch.equal(sc.view(torch.int32), ref_sc.view(torch.int32)), S
+        assert torch.equal(out, ref), S
+
+
+def test_planes_in_graph_replays_match_eager():
+    from dsa_amd import prepare_k
+    d = workloads.indexer_inputs(T=8, Hi=64, S=5000, seed=63)
+    g = workloads.to_device(d, DEV)
+    planes = prepare_k(g["k_idx"], g["k_scale"])
+    args = (g["q_idx"], None, None, g["weights"], g["causal_limit"])
+    eager = run_indexer_and_topk(*args, 256, k_planes=planes).clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run_indexer_and_topk(*args, 256, k_planes=planes)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = run_indexer_and_topk(*args, 256, k_planes=planes)
+    for _ in range(3):
+        out.fill_(-7)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
