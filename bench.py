@@ -54,6 +54,7 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 INT8_PEAK_TOPS = 5000.0      # dense int8 MFMA (= the fp8 dense peak)
 GRAPH_CALLS = 20
+WARMUP_S = 0.05              # minimum untimed warm-up (seconds of graph replays) per timing
 EXTRA_STEPS = 100            # timed calls per extra workload of the default run
 ATTN_CONFIGS = ("cfg1", "cfg2", "cfg3", "cfg4", "t1")
 # Workloads whose cache fits the 256 MB Infinity Cache also get a cold-cache
@@ -256,8 +257,15 @@ def time_graph(fn, steps, warmup, per=GRAPH_CALLS):
     full, rest = divmod(steps, per)
     g_full = graph_of(fn, per)
     g_rest = graph_of(fn, rest) if rest else None
-    for _ in range(max(1, -(-warmup // per))):
+    # untimed warm-up: at least `warmup` calls and about WARMUP_S of replays,
+    # so the first workload after a switch is not timed while the clocks and
+    # the address translation of its buffers are still settling
+    reps, t0 = 0, time.perf_counter()
+    while reps < max(1, -(-warmup // per)) or time.perf_counter() - t0 < WARMUP_S:
         g_full.replay()
+        reps += 1
+        if reps % 8 == 0 or reps >= max(1, -(-warmup // per)):
+            torch.cuda.synchronize()
     if g_rest is not None:
         g_rest.replay()
     torch.cuda.synchronize()

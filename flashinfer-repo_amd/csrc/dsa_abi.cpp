@@ -367,16 +367,13 @@ namespace dsa {
 IndexerWorkspace indexer_workspace_layout(int64_t T, int64_t Hi, int64_t S, bool own_scores,
                                           bool own_k) {
   IndexerWorkspace w = {};
-  const size_t kblocks = own_k ? (size_t)(S + 15) / 16 : 0, qblocks = (size_t)T * (size_t)(Hi / 16);
+  (void)Hi;
+  const size_t kblocks = own_k ? (size_t)(S + 15) / 16 : 0;
   size_t off = 0;
   w.k_pieces = off;
   off += up256(kblocks * 3 * 2 * 1024);
   w.k_max = off;
   off += up256(kblocks * 4);
-  w.q_pieces = off;
-  off += up256(qblocks * 4 * 2 * 1024);
-  w.q_max = off;
-  off += up256(qblocks * 4);
   w.k_cs = off;
   if (own_k) off += up256((size_t)S * 4);
   w.scores = off;
@@ -465,7 +462,7 @@ int dsa_indexer_topk(const dsa_indexer_args *a, void *stream) {
                 (long long)a->num_positions, (long long)a->k_planes_capacity);
   const dsa::IndexerWorkspace lay = dsa::indexer_workspace_layout(
       a->num_tokens, a->num_heads, a->num_positions, a->scores_out == nullptr, !prepared);
-  if (!a->workspace || a->workspace_bytes < lay.total || !aligned(a->workspace, 256))
+  if (lay.total > 0 && (!a->workspace || a->workspace_bytes < lay.total || !aligned(a->workspace, 256)))
     return fail(DSA_EWORKSPACE, "%s: workspace of %zu bytes (256-byte aligned) needed, got %zu",
                 fn, lay.total, a->workspace ? a->workspace_bytes : (size_t)0);
 
@@ -484,8 +481,6 @@ int dsa_indexer_topk(const dsa_indexer_args *a, void *stream) {
   p.page_size = (int32_t)(a->block_table ? a->page_size : 1);
   p.out = a->out;
   char *ws = static_cast<char *>(a->workspace);
-  p.q_pieces = reinterpret_cast<int8_t *>(ws + lay.q_pieces);
-  p.q_max = reinterpret_cast<int32_t *>(ws + lay.q_max);
   if (prepared) {
     const dsa::KPlanesLayout kl = dsa::k_planes_layout(a->k_planes_capacity);
     char *kp = static_cast<char *>(const_cast<void *>(a->k_planes));

@@ -33,17 +33,19 @@
 // 2^50).  e4m3fn NaN codes (0x7f, 0xff) count as zero.
 //
 // Kernels:
-//   dsa_idx_prep_kernel    q and k codes -> piece planes laid out as MFMA
-//                          operands in lane order (one 1 KB chunk per 16 rows,
-//                          piece and 64-wide k-step), plus the largest |x|
-//                          of every 16-row block, and c_s of every position
-//                          in a contiguous workspace array.  With a paged K
-//                          cache it reads each position's codes and scale
-//                          through the page map.
+//   dsa_idx_prep_kernel    k codes -> piece planes laid out as MFMA
+//                          operands in lane order (one 1 KB chunk per 16
+//                          positions, piece and 64-wide k-step), plus the
+//                          largest |x| of every 16-position block, and c_s
+//                          of every position (kept by the caller as prepared
+//                          K planes, or in the call's workspace).  With a
+//                          paged K cache it reads each position's codes and
+//                          scale through the page map.
 //   dsa_idx_score_kernel   two waves per query token, up to 4 tokens per
 //                          workgroup sharing a range of positions.  The
-//                          token's q pieces stay in registers (A operands,
-//                          heads as M); each 16-position block's k pieces are
+//                          token's q pieces are derived from its codes in
+//                          registers (A operands, heads as M, through a code
+//                          -> pieces table in LDS); each 16-position block's k pieces are
 //                          one coalesced 1 KB load per operand (B, positions
 //                          as N).  When every block of the range takes the
 //                          three-product int32 path, the token's two waves
@@ -86,7 +88,6 @@ constexpr int kIdxDim = 128;
 constexpr int kKTokenBytes = kIdxDim + 4;  // paged K cache: codes + fp32 scale per token
 constexpr int kChunk = 1024;              // one MFMA operand: 64 lanes x 16 bytes
 constexpr int kBlockBytes = 3 * 2 * kChunk;  // k block: 3 planes x 2 k-steps
-constexpr int kQBlockBytes = 4 * 2 * kChunk; // q head block: 4 planes x 2 k-steps
 constexpr int kPrepThreads = 256;         // four waves, one destination block each
 constexpr int kScoreWaves = 8;            // waves per score workgroup (two per token)
 constexpr int kTargetScoreWaves = 2048;   // two waves per SIMD on 256 CUs
@@ -122,122 +123,149 @@ __device__ __forceinline__ i32x4 mfma(i32x4 a, i32x4 b, i32x4 c) {
 }
 
 // ---- operand preparation -------------------------------------------------
-//
-// Destination blocks 0 .. k_blocks-1 are k blocks k_block0 .. (16 positions
-// each; none when the call uses prepared K planes); the following T*Hi/16 are
-// q head blocks (token t, head block hb).  One wave prepares one destination
-// block; lane l = 16*g + c loads the 2 x 16 bytes it
-// writes: row c at dims 64*ks + 16*g for k-steps ks = 0, 1, so every plane
-// store of the wave is one contiguous 1 KB operand chunk.
-//
-// An operand chunk holds, for lane l = 16*g + c, the 16 bytes of k-step ks
-// (64 dims) starting at dim 16*g: of position 16*block + c (B operand), or of
-// the head that MFMA row c of head block hb stands for (A operand).  MFMA row
-// 4*g' + i of head block hb is head g'*Hi/4 + 4*hb + i, so that the four
-// output rows a lane receives (rows 4g'..4g'+3) are consecutive heads of the
-// lane's head group g'.
-__global__ __launch_bounds__(kPrepThreads) void dsa_idx_prep_kernel(IndexerParams p) {
-  // code -> signed bytes p0 | p1 << 8 | p2 << 16 | (p0 - p1) << 24
-  __shared__ uint32_t lut[256];
-  {
-    const int x = e4m3_x(threadIdx.x);
-    const uint32_t b0 = piece_byte(x, 0), b1 = piece_byte(x, 1);
-    const uint32_t d = (uint32_t)((int)(int8_t)b0 - (int)(int8_t)b1) & 0xffu;
-    lut[threadIdx.x] = b0 | (b1 << 8) | (piece_byte(x, 2) << 16) | (d << 24);
-  }
-  __syncthreads();
-  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nqb = p.Hi >> 4;
-  const int total = p.k_blocks + p.T * nqb;
-  const int wblk = blockIdx.x * (kPrepThreads / 64) + wave;
-  if (wblk >= total) return;
-  const bool is_k = wblk < p.k_blocks;
-  const int blk = is_k ? p.k_block0 + wblk : wblk;  // k block index, or k_blocks + q block
 
-  uint4 raw[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
-  int8_t *dst;
-  if (is_k) {
-    const int s = blk * 16 + c;
-    if (s < p.S) {
-      if (p.k_cache != nullptr) {  // paged: codes and scale through the page map
-        const int pg = p.k_pages[s / p.k_page_size], off = s % p.k_page_size;
-        if ((uint32_t)pg < (uint32_t)p.k_num_pages) {
-          const uint8_t *page = p.k_cache + (int64_t)pg * p.k_page_size * kKTokenBytes;
-          raw[0] = *(const uint4 *)(page + off * kIdxDim + g * 16);
-          raw[1] = *(const uint4 *)(page + off * kIdxDim + 64 + g * 16);
-          if (g == 0) p.k_cs[s] = *(const float *)(page + p.k_page_size * kIdxDim + off * 4) * 0x1p-18f;
-        } else if (g == 0) {  // unmapped page: a zero row of scale 0
-          p.k_cs[s] = 0.0f;
-        }
-      } else {
-        const uint8_t *row = p.k + (int64_t)s * kIdxDim;
-        raw[0] = *(const uint4 *)(row + g * 16);
-        raw[1] = *(const uint4 *)(row + 64 + g * 16);
-        if (g == 0) p.k_cs[s] = p.k_scale[s] * 0x1p-18f;
-      }
-    }
-    dst = p.k_pieces + (int64_t)blk * kBlockBytes + lane * 16;
-  } else {
-    const int qb = wblk - p.k_blocks, t = qb / nqb, hb = qb % nqb;
-    const int head = (c >> 2) * (p.Hi >> 2) + 4 * hb + (c & 3);
-    const uint8_t *row = p.q + ((int64_t)t * p.Hi + head) * kIdxDim;
-    raw[0] = *(const uint4 *)(row + g * 16);
-    raw[1] = *(const uint4 *)(row + 64 + g * 16);
-    dst = p.q_pieces + (int64_t)qb * kQBlockBytes + lane * 16;
-  }
-  // e4m3 magnitudes order like their codes & 0x7f; the NaN code 0x7f ranks
-  // above 448, which only makes the block's bound conservative
-  const uint32_t w[8] = {raw[0].x, raw[0].y, raw[0].z, raw[0].w, raw[1].x, raw[1].y, raw[1].z, raw[1].w};
+// e4m3fn code -> its signed 7-bit pieces as bytes: p0 | p1 << 8 | p2 << 16 |
+// (p0 - p1) << 24 (the kernels keep this table in LDS).
+__device__ __forceinline__ uint32_t piece_word(uint32_t code) {
+  const int x = e4m3_x(code);
+  const uint32_t b0 = piece_byte(x, 0), b1 = piece_byte(x, 1);
+  const uint32_t d = (uint32_t)((int)(int8_t)b0 - (int)(int8_t)b1) & 0xffu;
+  return b0 | (b1 << 8) | (piece_byte(x, 2) << 16) | (d << 24);
+}
+
+// Largest |x| (x = value * 2^9) of a set of codes from its largest code &
+// 0x7f (e4m3 magnitudes order like their codes; the NaN code 0x7f ranks above
+// 448, which only makes a bound conservative).
+__device__ __forceinline__ int magnitude_bound(uint32_t top) {
+  return top == 0x7f ? (15 << 14) : e4m3_x(top);
+}
+
+// Wave-wide largest code & 0x7f of the 32 codes a lane holds in w[8].
+__device__ __forceinline__ uint32_t wave_top_code(const uint32_t (&w)[8]) {
   uint32_t mc = 0;
 #pragma unroll
   for (int i = 0; i < 32; ++i) mc = max(mc, (w[i >> 2] >> (8 * (i & 3))) & 0x7fu);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) mc = max(mc, (uint32_t)__shfl_xor((int)mc, o));
-  const uint32_t top = __builtin_amdgcn_readfirstlane(mc);
-  const int bmax = top == 0x7f ? (15 << 14) : e4m3_x(top);
-  const bool two = bmax < kTwoPieceLimit;
-  if (lane == 0) {
-    if (is_k) p.k_max[blk] = bmax;
-    else p.q_max[wblk - p.k_blocks] = bmax;
+  return __builtin_amdgcn_readfirstlane(mc);
+}
+
+// Plane `byte` of the LUT words v[32] of a lane's 2 x 16 codes (negated: the
+// plane's bytes negated), as the two k-steps' 16-byte operand pieces.
+__device__ __forceinline__ void pack_plane(const uint32_t (&v)[32], int byte, bool negate,
+                                           i32x4 (&out)[2]) {
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      uint32_t packed = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        uint32_t x = (v[16 * ks + 4 * d + b] >> (8 * byte)) & 0xffu;
+        if (negate) x = (0u - x) & 0xffu;
+        packed |= x << (8 * b);
+      }
+      out[ks][d] = (int)packed;
+    }
   }
+}
+
+// K blocks k_block0 .. k_block0 + k_blocks - 1 (16 positions each) -> piece
+// planes laid out as MFMA B operands in lane order (one 1 KB chunk per plane
+// and 64-wide k-step), the largest |x| of every block, and c_s of every
+// position.  One wave per block; lane l = 16*g + c loads the 2 x 16 bytes it
+// writes: position 16*block + c at dims 64*ks + 16*g for k-steps ks = 0, 1,
+// so every plane store of the wave is one contiguous 1 KB chunk.  Positions
+// at or past S read as zeros.
+__global__ __launch_bounds__(kPrepThreads) void dsa_idx_prep_kernel(IndexerParams p) {
+  __shared__ uint32_t lut[256];
+  lut[threadIdx.x] = piece_word(threadIdx.x);
+  __syncthreads();
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wblk = blockIdx.x * (kPrepThreads / 64) + wave;
+  if (wblk >= p.k_blocks) return;
+  const int blk = p.k_block0 + wblk;
+
+  uint4 raw[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+  const int s = blk * 16 + c;
+  if (s < p.S) {
+    if (p.k_cache != nullptr) {  // paged: codes and scale through the page map
+      const int pg = p.k_pages[s / p.k_page_size], off = s % p.k_page_size;
+      if ((uint32_t)pg < (uint32_t)p.k_num_pages) {
+        const uint8_t *page = p.k_cache + (int64_t)pg * p.k_page_size * kKTokenBytes;
+        raw[0] = *(const uint4 *)(page + off * kIdxDim + g * 16);
+        raw[1] = *(const uint4 *)(page + off * kIdxDim + 64 + g * 16);
+        if (g == 0) p.k_cs[s] = *(const float *)(page + p.k_page_size * kIdxDim + off * 4) * 0x1p-18f;
+      } else if (g == 0) {  // unmapped page: a zero row of scale 0
+        p.k_cs[s] = 0.0f;
+      }
+    } else {
+      const uint8_t *row = p.k + (int64_t)s * kIdxDim;
+      raw[0] = *(const uint4 *)(row + g * 16);
+      raw[1] = *(const uint4 *)(row + 64 + g * 16);
+      if (g == 0) p.k_cs[s] = p.k_scale[s] * 0x1p-18f;
+    }
+  }
+  int8_t *dst = p.k_pieces + (int64_t)blk * kBlockBytes + lane * 16;
+  const uint32_t w[8] = {raw[0].x, raw[0].y, raw[0].z, raw[0].w, raw[1].x, raw[1].y, raw[1].z, raw[1].w};
+  const int bmax = magnitude_bound(wave_top_code(w));
+  if (lane == 0) p.k_max[blk] = bmax;
 
   uint32_t v[32];
 #pragma unroll
   for (int i = 0; i < 32; ++i) v[i] = lut[(w[i >> 2] >> (8 * (i & 3))) & 0xffu];
-  // plane `slot` of both k-steps from LUT byte `byte` (negated: q's q1 - q0);
-  // non-temporal stores: the planes are read by the next kernel, and stores
-  // kept in L2 cost a write-back at the kernel's end (measured: 1.6 us of 10.8)
-  auto put = [&](int slot, int byte, bool negate) {
+  // p0, p1, then p2 if the block holds a value of magnitude >= 32, else
+  // p0 - p1 (slot 2 is read as p2 only for such blocks); non-temporal stores:
+  // the planes are read by the next kernel, and stores kept in L2 cost a
+  // write-back at the kernel's end (measured: 1.6 us of 10.8)
+  const int bytes[3] = {0, 1, bmax < kTwoPieceLimit ? 3 : 2};
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      uint32_t o[4];
+  for (int slot = 0; slot < 3; ++slot) {
+    i32x4 o[2];
+    pack_plane(v, bytes[slot], false, o);
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        uint32_t packed = 0;
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          uint32_t x = (v[16 * ks + 4 * d + b] >> (8 * byte)) & 0xffu;
-          if (negate) x = (0u - x) & 0xffu;
-          packed |= x << (8 * b);
-        }
-        o[d] = packed;
-      }
-      __builtin_nontemporal_store(u32x4{o[0], o[1], o[2], o[3]}, (u32x4 *)(dst + (slot * 2 + ks) * kChunk));
-    }
-  };
-  // k block: p0, p1, then p2 if the block holds a value of magnitude >= 32,
-  // else p0 - p1 (slot 2 is read as p2 only for such blocks).  q head block:
-  // p0, p1, p2, and in slot 3 p1 - p0 when every value of its 16 heads is
-  // below 32.
-  put(0, 0, false);
-  put(1, 1, false);
-  if (is_k) {
-    put(2, two ? 3 : 2, false);
-  } else {
-    put(2, 2, false);
-    if (two) put(3, 3, true);
+    for (int ks = 0; ks < 2; ++ks)
+      __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o[ks]),
+                                  (u32x4 *)(dst + (slot * 2 + ks) * kChunk));
   }
+}
+
+// The A operands of token t's head block hb, derived in registers from the
+// raw codes: lane l = 16*g + c holds MFMA row c, which stands for head
+// (c / 4) * Hi/4 + 4*hb + c % 4 (so the four output rows a lane receives,
+// rows 4g..4g+3, are consecutive heads of head group g), dims 64*ks + 16*g ..
+// +15 for k-steps ks = 0, 1.  Planes NPL of them, by LUT byte (4: p1 - p0).
+template <int NPL>
+__device__ __forceinline__ void q_operands(const IndexerParams &p, const uint32_t *lut, int t, int hb,
+                                           const int (&plane)[NPL], i32x4 (&out)[NPL][2]) {
+  const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+  const int head = (c >> 2) * (p.Hi >> 2) + 4 * hb + (c & 3);
+  const uint8_t *row = p.q + ((int64_t)t * p.Hi + head) * kIdxDim;
+  const uint4 r0 = *(const uint4 *)(row + g * 16), r1 = *(const uint4 *)(row + 64 + g * 16);
+  const uint32_t w[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+  uint32_t v[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) v[i] = lut[(w[i >> 2] >> (8 * (i & 3))) & 0xffu];
+#pragma unroll
+  for (int k = 0; k < NPL; ++k) pack_plane(v, plane[k] == 4 ? 3 : plane[k], plane[k] == 4, out[k]);
+}
+
+// Largest |x| over every code of token t (all heads), the same in every lane.
+__device__ __forceinline__ int q_magnitude_bound(const IndexerParams &p, int t) {
+  const int lane = threadIdx.x & 63;
+  const uint4 *src = (const uint4 *)(p.q + (int64_t)t * p.Hi * kIdxDim);
+  const int n16 = p.Hi * kIdxDim / 16;  // 16-byte pieces of the token's codes
+  uint32_t mc = 0;
+  for (int i = lane; i < n16; i += 64) {
+    const uint4 r = src[i];
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) mc = max(mc, (w[j >> 2] >> (8 * (j & 3))) & 0x7fu);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mc = max(mc, (uint32_t)__shfl_xor((int)mc, o));
+  return magnitude_bound(__builtin_amdgcn_readfirstlane(mc));
 }
 
 // ---- scores --------------------------------------------------------------
@@ -255,7 +283,8 @@ __device__ __forceinline__ float sum_lane_groups(float v) {
 // Scores of token t over the 16-position blocks [b0, b1).  NQP = pieces of
 // q in play (3 when the token holds a value of magnitude >= 32).
 template <int NHB, int NQP>
-__device__ __forceinline__ void score_range(const IndexerParams &p, int t, int b0, int b1, int qmax) {
+__device__ __forceinline__ void score_range(const IndexerParams &p, const uint32_t *lut, int t, int b0,
+                                            int b1, int qmax) {
   // The rounding order is part of the score's definition: no contraction of
   // the products and sums written below into fused multiply-adds (the one
   // fused step of the definition is the explicit fmaf).
@@ -269,14 +298,13 @@ __device__ __forceinline__ void score_range(const IndexerParams &p, int t, int b
 
   // A operands of this token: [head block][piece][k-step]
   i32x4 qa[NHB][NQP][2];
-  const int8_t *qsrc = p.q_pieces + (int64_t)t * NHB * kQBlockBytes + lane * 16;
+  {
+    int planes[NQP];
 #pragma unroll
-  for (int hb = 0; hb < NHB; ++hb)
+    for (int pc = 0; pc < NQP; ++pc) planes[pc] = pc;
 #pragma unroll
-    for (int pc = 0; pc < NQP; ++pc)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        qa[hb][pc][ks] = load_chunk(qsrc + hb * kQBlockBytes + (pc * 2 + ks) * kChunk);
+    for (int hb = 0; hb < NHB; ++hb) q_operands<NQP>(p, lut, t, hb, planes, qa[hb]);
+  }
   // weights of the lane's rows: heads g*Hi/4 + 4*hb + i
   float wl[NHB][4];
   const float *wsrc = p.w + (int64_t)t * p.Hi + g * (p.Hi >> 2);
@@ -472,8 +500,8 @@ __device__ __forceinline__ void mfma_valu_groups() {
 // loaded: a wave-uniform loaded value is moved to a scalar register right
 // after its load, a wait that would tie each prefetch to its own step.
 template <int NHB>
-__device__ __forceinline__ void score_range_fast(const IndexerParams &p, int t, int b0, int b1,
-                                                 int *claim, bool lead) {
+__device__ __forceinline__ void score_range_fast(const IndexerParams &p, const uint32_t *lut, int t,
+                                                 int b0, int b1, int *claim, bool lead) {
 #pragma clang fp contract(off)
   static_assert(NHB >= 2, "the epilogue runs two head blocks behind");
   const int lane = threadIdx.x & 63;
@@ -507,16 +535,13 @@ __device__ __forceinline__ void score_range_fast(const IndexerParams &p, int t, 
   if (B >= bend) return;
   int N = claim_chunk();  // the next one
 
-  // A operands [hb][q0, q1, q1 - q0][k-step] (q slots 0, 1, 3)
+  // A operands [hb][q0, q1, q1 - q0][k-step]
   i32x4 qa[NHB][3][2];
-  const int8_t *qsrc = p.q_pieces + (int64_t)t * NHB * kQBlockBytes + lane * 16;
+  {
+    const int planes[3] = {0, 1, 4};
 #pragma unroll
-  for (int hb = 0; hb < NHB; ++hb)
-#pragma unroll
-    for (int pl = 0; pl < 3; ++pl)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        qa[hb][pl][ks] = load_chunk(qsrc + hb * kQBlockBytes + ((pl == 2 ? 3 : pl) * 2 + ks) * kChunk);
+    for (int hb = 0; hb < NHB; ++hb) q_operands<3>(p, lut, t, hb, planes, qa[hb]);
+  }
   float wl[NHB][4];
   const float *wsrc = p.w + (int64_t)t * p.Hi + g * (p.Hi >> 2);
 #pragma unroll
@@ -681,10 +706,12 @@ __global__ __launch_bounds__(kScoreWaves * 64) void dsa_idx_score_kernel(Indexer
   // two waves per token: slot = the token's place in the workgroup, member
   // 0 or 1 (waves w and w + tpw, which the hardware places on one SIMD)
   __shared__ int claim[kScoreWaves / 2];
+  __shared__ uint32_t lut[256];  // code -> its pieces (piece_word)
   const int tpw = blockDim.x >> 7;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int slot = wave % tpw, member = wave / tpw;
   if (threadIdx.x < kScoreWaves / 2) claim[threadIdx.x] = 0;
+  for (int i = threadIdx.x; i < 256; i += blockDim.x) lut[i] = piece_word(i);
   __syncthreads();
   const int t = blockIdx.y * tpw + slot;
   const int nkb = (p.S + 15) >> 4;
@@ -694,11 +721,9 @@ __global__ __launch_bounds__(kScoreWaves * 64) void dsa_idx_score_kernel(Indexer
   // the general paths split the range in halves
   const int mid = b0 + (b1 - b0 + 1) / 2;
   const int h0 = member == 0 ? b0 : mid, h1 = member == 0 ? mid : b1;
-  int qmax = 0;
-#pragma unroll
-  for (int j = 0; j < NHB; ++j) qmax = max(qmax, p.q_max[t * NHB + j]);
+  const int qmax = q_magnitude_bound(p, t);
   if (qmax >= kTwoPieceLimit) {
-    if (h0 < h1) score_range<NHB, 3>(p, t, h0, h1, qmax);
+    if (h0 < h1) score_range<NHB, 3>(p, lut, t, h0, h1, qmax);
     return;
   }
   // the range's largest block bound decides whether every block takes the
@@ -712,11 +737,11 @@ __global__ __launch_bounds__(kScoreWaves * 64) void dsa_idx_score_kernel(Indexer
     rmax = __builtin_amdgcn_readfirstlane(rmax);
     const bool descriptors_fit = (int64_t)nkb * kBlockBytes < (1LL << 31);
     if (rmax < kTwoPieceLimit && (int64_t)qmax * rmax * kIdxDim < (1LL << 31) && descriptors_fit) {
-      score_range_fast<NHB>(p, t, b0, b1, &claim[slot], member == 0);
+      score_range_fast<NHB>(p, lut, t, b0, b1, &claim[slot], member == 0);
       return;
     }
   }
-  if (h0 < h1) score_range<NHB, 2>(p, t, h0, h1, qmax);
+  if (h0 < h1) score_range<NHB, 2>(p, lut, t, h0, h1, qmax);
 }
 
 // ---- top-k ---------------------------------------------------------------
@@ -1170,9 +1195,7 @@ hipError_t launch_k_append(const KAppendParams &p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_indexer_prepare_k(const IndexerParams &pin, hipStream_t stream) {
-  IndexerParams p = pin;
-  p.T = 0;  // k blocks only
+hipError_t launch_indexer_prepare_k(const IndexerParams &p, hipStream_t stream) {
   if (p.k_blocks <= 0) return hipSuccess;
   const int prep_blocks = (p.k_blocks + kPrepThreads / 64 - 1) / (kPrepThreads / 64);
   hipLaunchKernelGGL(dsa_idx_prep_kernel, dim3(prep_blocks), dim3(kPrepThreads), 0, stream, p);
@@ -1183,11 +1206,9 @@ hipError_t launch_indexer(const IndexerParams &pin, hipStream_t stream) {
   if (pin.T == 0) return hipSuccess;
   IndexerParams p = pin;
   const int nkb = (p.S + 15) / 16, nqb = p.Hi / 16;
-  // k blocks [k_block0, k_block0 + k_blocks) are prepared with the q blocks
-  // (none when the caller's prepared K planes are used)
-  const int prep_blocks = (p.k_blocks + p.T * nqb + kPrepThreads / 64 - 1) / (kPrepThreads / 64);
-  hipLaunchKernelGGL(dsa_idx_prep_kernel, dim3(prep_blocks), dim3(kPrepThreads), 0, stream, p);
-  hipError_t e = hipGetLastError();
+  // the K planes, unless the call reads prepared ones (the q operands are
+  // derived inside the score kernel)
+  hipError_t e = launch_indexer_prepare_k(p, stream);
   if (e != hipSuccess) return e;
   if (p.S > 0) {
     // tokens per workgroup (two waves each) and 16-position blocks per

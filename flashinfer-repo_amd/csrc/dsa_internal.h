@@ -110,8 +110,6 @@ size_t attn_split_workspace(int64_t T, int64_t H, int64_t K, int32_t requested);
 // Lightning indexer.  Workspace layout (see indexer_workspace_layout):
 //   k_pieces [ceil(S/16)][3 pieces][2 k-steps][1024 B]  MFMA B operands, lane order
 //   k_max    [ceil(S/16)]                               max |value * 2^9| per block
-//   q_pieces [T][Hi/16][4 planes][2 k-steps][1024 B]    MFMA A operands, lane order
-//   q_max    [T][Hi/16]                                 max |value * 2^9| per 16 heads
 //   k_cs     [S] fp32                                   c_s = fl32(k_scale * 2^-18) per position
 //   scores   [T][S] fp32                                (unless the caller's)
 struct IndexerParams {
@@ -136,8 +134,6 @@ struct IndexerParams {
   float *scores;          // [T][S] (workspace or caller buffer)
   int8_t *k_pieces;
   int32_t *k_max;
-  int8_t *q_pieces;
-  int32_t *q_max;
   int32_t blocks_per_wg;  // 16-position blocks one score workgroup walks (set by the launcher)
   // k blocks the prep kernel derives planes for: [k_block0, k_block0 + k_blocks)
   // (0 blocks when the call reads prepared K planes)
@@ -145,7 +141,7 @@ struct IndexerParams {
 };
 
 struct IndexerWorkspace {
-  size_t k_pieces, k_max, q_pieces, q_max, k_cs, scores, total;  // byte offsets; total = size
+  size_t k_pieces, k_max, k_cs, scores, total;  // byte offsets; total = size
 };
 
 // Offsets of the indexer's workspace regions; scores are left out when the

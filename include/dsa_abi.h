@@ -228,7 +228,9 @@ int dsa_attn_merge(const dsa_attn_merge_args *args, void *stream);
  *   optional (NULL = not returned; masked entries hold -inf).
  * head_dim must be 128, num_heads 16, 32, 48 or 64, topk <= 2^24.  The
  * workspace (dsa_indexer_workspace_bytes, 256-byte aligned) holds the MFMA
- * operand pieces of q and k and, unless scores_out is given, the scores.
+ * operand pieces of k and, unless scores_out is given, the scores (the q
+ * operands are derived inside the score kernel); a call whose workspace
+ * size is 0 may pass NULL.
  */
 typedef struct dsa_indexer_args {
   const uint8_t *q_idx;
@@ -336,8 +338,8 @@ int dsa_indexer_k_append(const dsa_k_append_args *args, void *stream);
 size_t dsa_indexer_workspace_bytes(int64_t num_tokens, int64_t num_heads, int64_t head_dim,
                                    int64_t num_positions);
 
-/* Workspace of a dsa_indexer_topk call that reads prepared K planes (the q
- * operand pieces and, unless scores_out is given, the scores). */
+/* Workspace of a dsa_indexer_topk call that reads prepared K planes: the
+ * scores, unless scores_out is given. */
 size_t dsa_indexer_workspace_bytes_prepared(int64_t num_tokens, int64_t num_heads,
                                             int64_t head_dim, int64_t num_positions);
 

@@ -241,19 +241,19 @@ def test_indexer_host_validation(kw, code, needle):
 def test_indexer_workspace_and_empty_call():
     lib = _lib.load()
     # k operand chunks (3 pieces x 2 k-steps x 1 KB per 16 positions) + block
-    # maxima, q operand chunks (per token and 16 heads) + their maxima, the
-    # per-position scales of a paged K cache, fp32 scores; each region
-    # 256-aligned
+    # maxima, the per-position scales, fp32 scores; each region 256-aligned
+    # (the q operands are derived inside the score kernel)
     def up(x):
         return (x + 255) // 256 * 256
 
-    kb, qb = 32768 // 16, 64 * 64 // 16
-    want = (up(kb * 6144) + up(kb * 4) + up(qb * 8192) + up(qb * 4) + up(32768 * 4)
-            + up(64 * 32768 * 4))
+    kb = 32768 // 16
+    want = up(kb * 6144) + up(kb * 4) + up(32768 * 4) + up(64 * 32768 * 4)
     assert lib.dsa_indexer_workspace_bytes(64, 64, 128, 32768) == want
-    kb, qb = (1000 + 15) // 16, 3 * 48 // 16
-    want = up(kb * 6144) + up(kb * 4) + up(qb * 8192) + up(qb * 4) + up(1000 * 4) + up(3 * 1000 * 4)
+    kb = (1000 + 15) // 16
+    want = up(kb * 6144) + up(kb * 4) + up(1000 * 4) + up(3 * 1000 * 4)
     assert lib.dsa_indexer_workspace_bytes(3, 48, 128, 1000) == want
+    # with prepared K planes only the scores remain
+    assert lib.dsa_indexer_workspace_bytes_prepared(3, 48, 128, 1000) == up(3 * 1000 * 4)
     assert lib.dsa_indexer_topk(ctypes.byref(_idx_args(num_tokens=0, q_idx=None)), None) == 0
 
 

@@ -152,6 +152,28 @@ def test_tied_top_group_every_selection_path(n_tied, topk):
             assert np.array_equal(got_idx[t], want), f"row {t}"
 
 
+@pytest.mark.parametrize("topk", [1, 64, 1000])
+def test_outlier_scores_crowd_the_linear_bins(topk):
+    """A few huge scores stretch the row's score range, so the top-k's
+    histogram of 2048 bins linear in the score puts nearly every key in a
+    handful of bins and the k-th largest's bin is crowded: the selection
+    must fall back to its radix passes and stay exact (rows 0-1); row 2 has
+    an ordinary spread."""
+    g = torch.Generator().manual_seed(71)
+    T, Hi, S = 3, 16, 6000
+    q = torch.ones(T, Hi, 128)
+    q[2] = torch.randn(Hi, 128, generator=g)
+    k = torch.randn(S, 128, generator=g)
+    k[[17, 4000, 5999]] = 400.0                        # dot ~ 51200 against ~N(0, 11)
+    d = {"q_idx": workloads.e4m3(q), "k_idx": workloads.e4m3(k),
+         "k_scale": torch.ones(S), "weights": torch.full((T, Hi), 1.0 / Hi),
+         "causal_limit": torch.tensor([S - 1, S - 2, S - 1], dtype=torch.int32)}
+    print(f"outlier scores k={topk}", flush=True)
+    got_idx, got_sc = _gpu_indexer(d, topk)
+    ref_idx, ref_sc = _oracle(d, topk)
+    _assert_same(got_idx, got_sc, ref_idx, ref_sc, f"outliers k={topk}")
+
+
 def test_large_values_take_the_wide_paths():
     """|value| >= 32 needs the third 7-bit piece (fp64 combine), and large
     dots overflow the int32 fast combine; both must stay exact."""
