@@ -94,6 +94,8 @@ def parse():
                          "the GPU)")
     ap.add_argument("--profile-configs", default=",".join(ATTN_CONFIGS + ("cfg5",)),
                     help="workloads --record-profiles covers (comma-separated)")
+    ap.add_argument("--profiles-dir", default=os.path.join(ROOT, "profiles"),
+                    help="where --record-profiles writes traffic.json and the summaries")
     return ap.parse_args()
 
 
@@ -468,8 +470,8 @@ def measure_indexer(steps, warmup):
                      "unit": "TFLOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4),
                      "traffic": load_traffic("cfg5"), "counters": load_counters("cfg5"),
                      "algorithmic_ops": ops,
-                     "kernel": "dsa_idx_prep_kernel (q planes) + dsa_idx_score_kernel (timed "
-                               "via dsa_indexer_topk with topk=0 and prepared K planes)"},
+                     "kernel": "dsa_idx_score_kernel (timed via dsa_indexer_topk with topk=0 "
+                               "and prepared K planes; the q operands are derived inside it)"},
     }
     return fields, d
 
@@ -507,17 +509,17 @@ CALIBRATION_BYTES = 1 << 28
 
 def _short_name(name: str) -> str:
     """Kernel name without namespaces and parameter list."""
-    base = name.split("(")[0]
-    return base.replace("void ", "").replace("dsa::(anonymous namespace)::", "").strip()
+    base = name.replace("(anonymous namespace)::", "").replace("void ", "").replace("dsa::", "")
+    return base.split("(")[0].strip()
 
 
 def _dominant(config: str, names):
-    """The kernels that make up a workload's measured launch: for attention
-    the gather-attention kernel (not the merge kernel), for cfg5 the
-    per-call operand preparation plus the score kernel (the timed score
-    step)."""
+    """The kernel of a workload's measured launch: for attention the
+    gather-attention kernel (not the merge kernel), for cfg5 the score kernel
+    (the timed score step, which reads prepared K planes and derives the q
+    operands itself)."""
     if config == "cfg5":
-        return sorted(n for n in names if "dsa_idx_prep" in n or "dsa_idx_score" in n)
+        return [n for n in names if "dsa_idx_score" in n][:1]
     return [n for n in names if n.startswith("dsa_attn_") and "combine" not in n][:1]
 
 
@@ -554,12 +556,14 @@ def _counters(path):
     return {k: {c: statistics.median(v) for c, v in d.items()} for k, d in agg.items()}
 
 
-def record_profiles(out_dir: str, configs) -> None:
-    """Runs the profiler over every workload and writes profiles/traffic.json
-    and profiles/<kernel>_<workload>.txt from what it measured."""
+def record_profiles(out_dir: str, configs, profiles_dir: str) -> None:
+    """Runs the profiler over every workload and writes
+    <profiles_dir>/traffic.json and <profiles_dir>/<kernel>_<workload>.txt
+    from what it measured (an existing traffic.json there is updated)."""
     import csv
     out_dir = os.path.abspath(out_dir)
     os.makedirs(out_dir, exist_ok=True)
+    os.makedirs(profiles_dir, exist_ok=True)
     bench = [sys.executable, os.path.join(ROOT, "bench.py")]
     calib = {}
     cal_cmds = []
@@ -573,7 +577,7 @@ def record_profiles(out_dir: str, configs) -> None:
         calib[ctr] = (CALIBRATION_BYTES / 1024.0) / kib  # KiB per KiB the counter reads
     cal_note = (f"FETCH_SIZE x{calib['FETCH_SIZE']:.4f}, WRITE_SIZE x{calib['WRITE_SIZE']:.4f} "
                 f"(plain device copy of {CALIBRATION_BYTES} bytes)")
-    path = os.path.join(ROOT, "profiles", "traffic.json")
+    path = os.path.join(profiles_dir, "traffic.json")
     try:
         with open(path) as f:
             table = json.load(f)
@@ -638,7 +642,7 @@ def record_profiles(out_dir: str, configs) -> None:
                   + (f"{mfma:.4f}" if mfma is not None else "n/a"),
                   "L2 hit (TCC_HIT / (TCC_HIT + TCC_MISS)): "
                   + (f"{hits / (hits + miss):.4f}" if hits + miss else "n/a")]
-        with open(os.path.join(ROOT, "profiles", summary_file), "w") as f:
+        with open(os.path.join(profiles_dir, summary_file), "w") as f:
             f.write("\n".join(lines) + "\n")
         with open(path, "w") as f:
             json.dump(table, f, indent=1)
@@ -652,7 +656,8 @@ def main():
         copy_calibration(a.copy_calibration)
         return
     if a.record_profiles:
-        record_profiles(a.record_profiles, [c for c in a.profile_configs.split(",") if c])
+        record_profiles(a.record_profiles, [c for c in a.profile_configs.split(",") if c],
+                        a.profiles_dir)
         return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
