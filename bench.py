@@ -151,8 +151,8 @@ def load_counters(config: str):
     ent = load_record(config)
     if not ent:
         return None
-    return {k: ent.get(k) for k in ("mfma_busy_frac", "l2_hit_frac", "fetch_bytes_per_launch",
-                                    "write_bytes_per_launch", "source")}
+    return {k: ent.get(k) for k in ("mfma_busy_frac", "l2_hit_frac", "lds_busy_frac",
+                                    "fetch_bytes_per_launch", "write_bytes_per_launch", "source")}
 
 
 def host_cpu():
@@ -503,7 +503,9 @@ IDX_DATA = "synthetic (seeded; q_idx,k_idx ~N(0,1) as e4m3, scale~U(0.5,2), w~N(
 PROFILE_STEPS = ["--steps", "40", "--warmup", "5", "--no-cpu-baseline", "--cold-copies", "0"]
 COUNTER_PASSES = (("FETCH_SIZE",), ("WRITE_SIZE",),
                   ("SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CU_CYCLES", "SQ_INSTS_MFMA"),
-                  ("TCC_HIT_sum", "TCC_MISS_sum"))
+                  ("TCC_HIT_sum", "TCC_MISS_sum"),
+                  ("SQ_LDS_IDX_ACTIVE", "SQ_LDS_BANK_CONFLICT", "GRBM_GUI_ACTIVE"))
+NUM_CU = 256
 CALIBRATION_BYTES = 1 << 28
 
 
@@ -540,15 +542,17 @@ def _rocprof(args, out_dir, tag, program, log):
 
 def _counters(path):
     """{kernel: {counter: median over dispatches}} of a counter pass (values of
-    one dispatch summed over the counter's instances)."""
+    one dispatch summed over the counter's instances; GRBM_* counters, which
+    every XCD reports for the whole dispatch, take the largest instance)."""
     import collections
     import csv
     import statistics
     per = collections.defaultdict(lambda: collections.defaultdict(float))
     with open(path) as f:
         for r in csv.DictReader(f):
-            per[(r["Dispatch_Id"], _short_name(r["Kernel_Name"]))][r["Counter_Name"]] += \
-                float(r["Counter_Value"])
+            name, v = r["Counter_Name"], float(r["Counter_Value"])
+            cell = per[(r["Dispatch_Id"], _short_name(r["Kernel_Name"]))]
+            cell[name] = max(cell[name], v) if name.startswith("GRBM_") else cell[name] + v
     agg = collections.defaultdict(lambda: collections.defaultdict(list))
     for (_, k), v in per.items():
         for c, x in v.items():
@@ -609,6 +613,9 @@ def record_profiles(out_dir: str, configs, profiles_dir: str) -> None:
         busy = ctr.get("SQ_BUSY_CU_CYCLES", 0.0)
         mfma = ctr.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / (4 * busy) if busy else None
         hits, miss = ctr.get("TCC_HIT_sum", 0.0), ctr.get("TCC_MISS_sum", 0.0)
+        gui = ctr.get("GRBM_GUI_ACTIVE", 0.0)
+        lds = ctr.get("SQ_LDS_IDX_ACTIVE", 0.0) / (gui * NUM_CU) if gui else None
+        ldsc = ctr.get("SQ_LDS_BANK_CONFLICT", 0.0) / (gui * NUM_CU) if gui else None
         name = dom[-1] if dom else "none"
         summary_file = f"{name.split('<')[0]}_{c}.txt"
         dur = {n: avg for n, _, avg, *_ in stats}
@@ -620,6 +627,8 @@ def record_profiles(out_dir: str, configs, profiles_dir: str) -> None:
             "hbm_bytes_per_launch": int(round(fetch + write)),
             "mfma_busy_frac": round(mfma, 4) if mfma is not None else None,
             "l2_hit_frac": round(hits / (hits + miss), 4) if hits + miss else None,
+            "lds_busy_frac": round(lds, 4) if lds is not None else None,
+            "lds_bank_conflict_frac": round(ldsc, 4) if ldsc is not None else None,
             "calibration": cal_note,
             "csrc_sha256": digest,
             "source": f"profiles/{summary_file}",
@@ -641,7 +650,10 @@ def record_profiles(out_dir: str, configs, profiles_dir: str) -> None:
                   f"MFMA busy (SQ_VALU_MFMA_BUSY_CYCLES / (4 x SQ_BUSY_CU_CYCLES)): "
                   + (f"{mfma:.4f}" if mfma is not None else "n/a"),
                   "L2 hit (TCC_HIT / (TCC_HIT + TCC_MISS)): "
-                  + (f"{hits / (hits + miss):.4f}" if hits + miss else "n/a")]
+                  + (f"{hits / (hits + miss):.4f}" if hits + miss else "n/a"),
+                  "LDS busy (SQ_LDS_IDX_ACTIVE / (GRBM_GUI_ACTIVE x 256 CUs)): "
+                  + (f"{lds:.4f}" if lds is not None else "n/a")
+                  + ", bank-conflict cycles " + (f"{ldsc:.4f}" if ldsc is not None else "n/a")]
         with open(os.path.join(profiles_dir, summary_file), "w") as f:
             f.write("\n".join(lines) + "\n")
         with open(path, "w") as f:
