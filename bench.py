@@ -152,7 +152,8 @@ def load_counters(config: str):
     if not ent:
         return None
     return {k: ent.get(k) for k in ("mfma_busy_frac", "l2_hit_frac", "lds_busy_frac",
-                                    "fetch_bytes_per_launch", "write_bytes_per_launch", "source")}
+                                    "lds_bank_conflict_frac", "fetch_bytes_per_launch",
+                                    "write_bytes_per_launch", "source")}
 
 
 def host_cpu():
@@ -504,8 +505,7 @@ PROFILE_STEPS = ["--steps", "40", "--warmup", "5", "--no-cpu-baseline", "--cold-
 COUNTER_PASSES = (("FETCH_SIZE",), ("WRITE_SIZE",),
                   ("SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CU_CYCLES", "SQ_INSTS_MFMA"),
                   ("TCC_HIT_sum", "TCC_MISS_sum"),
-                  ("SQ_LDS_IDX_ACTIVE", "SQ_LDS_BANK_CONFLICT", "GRBM_GUI_ACTIVE"))
-NUM_CU = 256
+                  ("SQ_LDS_IDX_ACTIVE", "SQ_LDS_BANK_CONFLICT"))
 CALIBRATION_BYTES = 1 << 28
 
 
@@ -542,17 +542,15 @@ def _rocprof(args, out_dir, tag, program, log):
 
 def _counters(path):
     """{kernel: {counter: median over dispatches}} of a counter pass (values of
-    one dispatch summed over the counter's instances; GRBM_* counters, which
-    every XCD reports for the whole dispatch, take the largest instance)."""
+    one dispatch summed over the counter's instances)."""
     import collections
     import csv
     import statistics
     per = collections.defaultdict(lambda: collections.defaultdict(float))
     with open(path) as f:
         for r in csv.DictReader(f):
-            name, v = r["Counter_Name"], float(r["Counter_Value"])
-            cell = per[(r["Dispatch_Id"], _short_name(r["Kernel_Name"]))]
-            cell[name] = max(cell[name], v) if name.startswith("GRBM_") else cell[name] + v
+            per[(r["Dispatch_Id"], _short_name(r["Kernel_Name"]))][r["Counter_Name"]] += \
+                float(r["Counter_Value"])
     agg = collections.defaultdict(lambda: collections.defaultdict(list))
     for (_, k), v in per.items():
         for c, x in v.items():
@@ -613,9 +611,11 @@ def record_profiles(out_dir: str, configs, profiles_dir: str) -> None:
         busy = ctr.get("SQ_BUSY_CU_CYCLES", 0.0)
         mfma = ctr.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / (4 * busy) if busy else None
         hits, miss = ctr.get("TCC_HIT_sum", 0.0), ctr.get("TCC_MISS_sum", 0.0)
-        gui = ctr.get("GRBM_GUI_ACTIVE", 0.0)
-        lds = ctr.get("SQ_LDS_IDX_ACTIVE", 0.0) / (gui * NUM_CU) if gui else None
-        ldsc = ctr.get("SQ_LDS_BANK_CONFLICT", 0.0) / (gui * NUM_CU) if gui else None
+        # LDS cycles summed over the CUs, against the CUs' busy cycles; bank
+        # conflicts as a share of the LDS cycles
+        lds_active = ctr.get("SQ_LDS_IDX_ACTIVE", 0.0)
+        lds = lds_active / busy if busy else None
+        ldsc = ctr.get("SQ_LDS_BANK_CONFLICT", 0.0) / lds_active if lds_active else None
         name = dom[-1] if dom else "none"
         summary_file = f"{name.split('<')[0]}_{c}.txt"
         dur = {n: avg for n, _, avg, *_ in stats}
@@ -651,9 +651,10 @@ def record_profiles(out_dir: str, configs, profiles_dir: str) -> None:
                   + (f"{mfma:.4f}" if mfma is not None else "n/a"),
                   "L2 hit (TCC_HIT / (TCC_HIT + TCC_MISS)): "
                   + (f"{hits / (hits + miss):.4f}" if hits + miss else "n/a"),
-                  "LDS busy (SQ_LDS_IDX_ACTIVE / (GRBM_GUI_ACTIVE x 256 CUs)): "
+                  "LDS busy (SQ_LDS_IDX_ACTIVE / SQ_BUSY_CU_CYCLES): "
                   + (f"{lds:.4f}" if lds is not None else "n/a")
-                  + ", bank-conflict cycles " + (f"{ldsc:.4f}" if ldsc is not None else "n/a")]
+                  + "; bank-conflict share of LDS cycles (SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE): "
+                  + (f"{ldsc:.4f}" if ldsc is not None else "n/a")]
         with open(os.path.join(profiles_dir, summary_file), "w") as f:
             f.write("\n".join(lines) + "\n")
         with open(path, "w") as f:

@@ -64,10 +64,10 @@
 //
 // Within a 16-key block, MFMA row m of S^T holds key pi(m) = 8*((m>>2)&1) +
 // (m>>3) + 2*(m&3), so lane group g owns keys kbase(g) + {0,2,4,6} with
-// kbase = 0, 8, 1, 9.  The QK operand reads still touch 16 distinct rows
-// (conflict-free with the 1040-byte pitch), and the PV transpose reads of one
-// 32-lane half touch 8 rows whose 32-byte pieces land on 8 disjoint bank
-// ranges, which is conflict-free too.
+// kbase = 0, 8, 1, 9.  The QK operand reads touch 16 distinct rows and the PV
+// transpose reads of one 32-lane half 8 rows whose 32-byte pieces land on
+// disjoint bank ranges; the row layouts below keep both free of bank
+// conflicts.
 //
 // ds_read_b64_tr_b16, per 16-lane group: lane i receives element i%4 of the
 // 4-element (8-byte) rows addressed by lanes 4j + i/4, j = 0..3.  Pointing
@@ -91,13 +91,25 @@ typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kBufferFlags = 0x00020000;
 constexpr int kSC1 = 16;
 
-// LDS geometry (bytes).  A ckv row is padded from 1024 to 1040 B so the 16
-// rows one MFMA operand read touches fall in distinct banks; kpe rows are
+// LDS geometry (bytes).  gfx950's LDS serves a ds_read_b128 32 lanes at a
+// time over 128 four-byte banks (512 bytes): the 32 lanes' 16-byte pieces must
+// fall on distinct 16-byte columns of a 512-byte line (measured: a colliding
+// pair doubles the instruction's LDS cycles).  An MFMA operand read takes
+// 16-byte piece g of 16 rows in lane group g (g = 0, 1 in a half), so rows at a
+// pitch of 1024 + 16 B put piece 1 of row r on the column of piece 0 of row
+// r + 1.  The ring kernel keeps that pitch and stores key k of a 32-key tile
+// at row ring_row(k) = 2 (k mod 16) + k / 16 (a 16-key block on every other
+// row: columns 2r + g); the wave kernel holds 16-key blocks and pads its rows
+// to 1024 + 32 B instead (kWavePitch).  Both place the transposing V^T reads
+// (8-byte pieces, 32 lanes a time) on distinct columns as well.  kpe rows are
 // gathered 8 per DMA instruction in chunk-major order (lane i of the DMA holds
-// 16-byte chunk i/8 of row i%8), so a column read of 16 rows hits 16
-// consecutive chunks.
+// 16-byte chunk i/8 of row i%8); group q of a tile starts at
+// kpe_group_off(q), odd groups 128 B further, so the two groups one 16-key
+// block reads fall on different halves of the line.
 constexpr int kCkvPitch = 1024 + 16;
 constexpr int kKpeGroupPitch = 1024 + 128;
+__device__ __forceinline__ int ring_row(int k) { return 2 * (k & 15) + (k >> 4); }
+__device__ __forceinline__ int kpe_group_off(int q) { return q * kKpeGroupPitch + (q & 1) * 128; }
 constexpr int kCkvStageBytes = kKeysPerTile * kCkvPitch;
 constexpr int kStageBytes = kCkvStageBytes + (kKeysPerTile / 8) * kKpeGroupPitch;
 constexpr int kStages = 4;
@@ -379,7 +391,7 @@ struct FusedAddr {
 
 template <int K>
 __device__ __forceinline__ void fused_issue(const FusedAddr &a, u32x4 &kq, u32x2 (&vt)[2]) {
-  constexpr int kRowB = 16 * kCkvPitch;  // key block 1 of the V^T reads
+  constexpr int kRowB = kCkvPitch;  // key block 1 of the V^T reads: the next row (ring_row)
   constexpr int kStep = K % 18;
   constexpr int kOff = kStep < 16 ? kStep * 64 : (kStep - 16) * 512;
   const uint32_t qa = K < 18 ? (kStep < 16 ? a.qa0 : a.ka0) : (kStep < 16 ? a.qa1 : a.ka1);
@@ -738,17 +750,17 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
   };
   auto fire_tile = [&](int j, const TileSrc &a) {
     char *st = lds + (j & (kStages - 1)) * kStageBytes;
-    char *kdst = st + kCkvStageBytes + grp * kKpeGroupPitch;
+    char *kdst = st + kCkvStageBytes + kpe_group_off(grp);
     if constexpr (NARROW) {
 #pragma unroll
       for (int m = 0; m < R::kRows; ++m)
-        lds_dma16_buf(ckv_rsrc, st + (grp * 8 + row0 + m) * kCkvPitch, a.row[m] + lane * 16);
+        lds_dma16_buf(ckv_rsrc, st + ring_row(grp * 8 + row0 + m) * kCkvPitch, a.row[m] + lane * 16);
       if (kpe_lane) lds_dma16_buf(kpe_rsrc, kdst, a.ko);
     } else {
 #pragma unroll
       for (int m = 0; m < R::kRows; ++m) {
         const char *src = (const char *)readlane64(a.ckv, row0 + m) + lane * 16;
-        lds_dma16(src, st + (grp * 8 + row0 + m) * kCkvPitch);
+        lds_dma16(src, st + ring_row(grp * 8 + row0 + m) * kCkvPitch);
       }
       if (kpe_lane) lds_dma16((const char *)a.kpe + (lane >> 3) * 16, kdst);
     }
@@ -768,8 +780,8 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
     for (int bb = 0; bb < R::kBlocks; ++bb) {
       const int b = qb0 + bb;
       const int kk = b * 16 + key_of_row(r16);
-      const char *rowp = st_ckv + kk * kCkvPitch + g * 16;
-      const char *kp = st_kpe + (kk >> 3) * kKpeGroupPitch + (kk & 7) * 16;
+      const char *rowp = st_ckv + ring_row(kk) * kCkvPitch + g * 16;
+      const char *kp = st_kpe + kpe_group_off(kk >> 3) + (kk & 7) * 16;
       sacc[bb] = qk_part<R::kParts>(part, rowp, kp, qreg, g);
     }
   };
@@ -848,16 +860,16 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
   auto pv = [&](const char *st_ckv, const bf16x8 &p_hi, const bf16x8 &p_lo) {
     // ---- O^T += V^T . P^T over this wave's feature slice; k-slot k of lane
     // group g is key kbase+2k (k < 4) or 16+kbase+2(k-4).  Lane 16g+s points
-    // the transpose read at key row kbase + 2*(s/4) (+16 for slots 4..7),
-    // features f0 + 4*(s%4).  Scheduling barriers every four feature blocks
+    // the transpose read at key kbase + 2*(s/4) (+16 for slots 4..7: the next
+    // LDS row, ring_row), features f0 + 4*(s%4).  Scheduling barriers every four feature blocks
     // keep the compiler from hoisting all reads of a wide slice (FS == 1:
     // 64 of them) ahead of the MFMAs.
-    const char *vsrc = st_ckv + (kbase + 2 * (r16 >> 2)) * kCkvPitch +
+    const char *vsrc = st_ckv + ring_row(kbase + 2 * (r16 >> 2)) * kCkvPitch +
                        (fs * R::kNFB * 16 + 4 * (r16 & 3)) * 2;
     // The reads are tr_read4 batches (inline asm): with the builtin form the
     // compiler waits for every outstanding LDS DMA (vmcnt(0)) before the
     // first read, which drains the gathers in flight on every tile.
-    for_tr_batches<R::kNFB, 16 * kCkvPitch>(vsrc, [&](int f0, const bf16x8(&av)[4]) {
+    for_tr_batches<R::kNFB, kCkvPitch>(vsrc, [&](int f0, const bf16x8(&av)[4]) {
 #pragma unroll
       for (int f = 0; f < 4; ++f) {
         const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[f], p_hi, acc[f0 + f], 0, 0, 0);
@@ -912,10 +924,10 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
       const char *st_prev = lds + ((i + kStages - 1) & (kStages - 1)) * kStageBytes;
       const char *st_kpe = st_ckv + kCkvStageBytes;
       const FusedAddr fa = {
-          lds_addr(st_ckv + k0 * kCkvPitch + g * 16), lds_addr(st_ckv + k1 * kCkvPitch + g * 16),
-          lds_addr(st_kpe + (k0 >> 3) * kKpeGroupPitch + (k0 & 7) * 16 + g * 128),
-          lds_addr(st_kpe + (k1 >> 3) * kKpeGroupPitch + (k1 & 7) * 16 + g * 128),
-          lds_addr(st_prev + (kbase + 2 * (r16 >> 2)) * kCkvPitch + 4 * (r16 & 3) * 2)};
+          lds_addr(st_ckv + ring_row(k0) * kCkvPitch + g * 16), lds_addr(st_ckv + ring_row(k1) * kCkvPitch + g * 16),
+          lds_addr(st_kpe + kpe_group_off(k0 >> 3) + (k0 & 7) * 16 + g * 128),
+          lds_addr(st_kpe + kpe_group_off(k1 >> 3) + (k1 & 7) * 16 + g * 128),
+          lds_addr(st_prev + ring_row(kbase + 2 * (r16 >> 2)) * kCkvPitch + 4 * (r16 & 3) * 2)};
       qk_pv_tile(fa, qreg, p_hi, p_lo, acc, sacc);
     };
     // Both teams run the same loop (X_j, fused j, Y_j, softmax j); team B
@@ -982,10 +994,10 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
         // part reads the zeroed stage with zero probabilities)
         const char *st_kpe = st_ckv + kCkvStageBytes;
         const FusedAddr fa = {
-            lds_addr(st_ckv + k0 * kCkvPitch + g * 16), lds_addr(st_ckv + k1 * kCkvPitch + g * 16),
-            lds_addr(st_kpe + (k0 >> 3) * kKpeGroupPitch + (k0 & 7) * 16 + g * 128),
-            lds_addr(st_kpe + (k1 >> 3) * kKpeGroupPitch + (k1 & 7) * 16 + g * 128),
-            lds_addr(lds + st_prev + (kbase + 2 * (r16 >> 2)) * kCkvPitch + 4 * (r16 & 3) * 2)};
+            lds_addr(st_ckv + ring_row(k0) * kCkvPitch + g * 16), lds_addr(st_ckv + ring_row(k1) * kCkvPitch + g * 16),
+            lds_addr(st_kpe + kpe_group_off(k0 >> 3) + (k0 & 7) * 16 + g * 128),
+            lds_addr(st_kpe + kpe_group_off(k1 >> 3) + (k1 & 7) * 16 + g * 128),
+            lds_addr(lds + st_prev + ring_row(kbase + 2 * (r16 >> 2)) * kCkvPitch + 4 * (r16 & 3) * 2)};
         qk_pv_tile(fa, qreg, p_hi, p_lo, acc, sacc);
       } else {
         scores(st_ckv, sacc);
@@ -1086,14 +1098,15 @@ __global__ __launch_bounds__(W * 64, 1) void dsa_attn_ring_kernel(AttnParams p) 
 // values of key rows 4g..4g+3, whose V^T values (the A operand, repeated for
 // the lo slots) are one ds_read_b64_tr_b16 per feature block.
 //
-// Stage layout: 16 ckv rows at a 1040-byte pitch (key k at row k), then the
+// Stage layout: 16 ckv rows at a 1056-byte pitch (key k at row k), then the
 // 16 kpe rows chunk-major (16-byte chunk c of key k at 256 c + 16 k), so the
 // QK operand reads (16 rows, one column) and the transposing V^T reads (rows
 // key_of_row(4g + j)) are free of bank conflicts.
+constexpr int kWavePitch = 1024 + 32;
 constexpr int kWaveBlock = 16;                          // keys per block
 constexpr int kWaveWaves = 4;
-constexpr int kWaveKpeOff = kWaveBlock * kCkvPitch;     // 16640
-constexpr int kWaveStage = kWaveKpeOff + kWaveBlock * 128;  // + 2048 = 18688
+constexpr int kWaveKpeOff = kWaveBlock * kWavePitch;     // 16896
+constexpr int kWaveStage = kWaveKpeOff + kWaveBlock * 128;  // + 2048 = 18944
 constexpr int kWaveRing = 2 * kWaveStage;
 constexpr int kWaveIds = kMaxChunkWide;                 // slot ids of a chunk, staged once
 constexpr int kWaveSortBlocks = 16;  // a wave sorts its keys by slot from this many blocks on
@@ -1224,19 +1237,19 @@ __global__ __launch_bounds__(kWaveWaves * 64, 1) void dsa_attn_wave_kernel(AttnP
   // traffic of every wave loading all of it, and issued after the ids are
   // stored, so the id loads that store waits for are not queued behind it;
   // issued right after the id loads instead it gained nothing): wave w DMAs the
-  // q_nope rows of heads 4w .. 4w+3 (pitch 1040 bytes: the 16 heads' reads
-  // of one k-step land on distinct banks) and their q_pe rows (pitch 128)
+  // q_nope rows of heads 4w .. 4w+3 (at the stage's row pitch: the 16 heads'
+  // reads of one k-step land on distinct banks) and their q_pe rows (pitch 128)
   // into the second stage of wave 0's ring, which the loop first fills with
   // wave 0's second block.
   char *qstage = lds + kWaveStage;
-  constexpr int kQPePos = kHeadsPerGroup * kCkvPitch;  // q_pe rows after the 16 q_nope rows
+  constexpr int kQPePos = kHeadsPerGroup * kWavePitch;  // q_pe rows after the 16 q_nope rows
   static_assert(kQPePos + kHeadsPerGroup * 128 <= kWaveStage, "Q staging fits one stage");
   {
     const int hb = blockIdx.y * kHeadsPerGroup;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int h = 4 * wave + i;
-      lds_dma16(p.q_nope + t * p.qn_st + (hb + h) * p.qn_sh + lane * 16, qstage + h * kCkvPitch);
+      lds_dma16(p.q_nope + t * p.qn_st + (hb + h) * p.qn_sh + lane * 16, qstage + h * kWavePitch);
     }
     if (lane < 32) {
       const int h = 4 * wave + (lane >> 3);
@@ -1264,7 +1277,7 @@ __global__ __launch_bounds__(kWaveWaves * 64, 1) void dsa_attn_wave_kernel(AttnP
       const uint32_t ko = (id >= 0 ? __umul24((uint32_t)id, p.kpe_rs) : kOOB) + g * 16;
 #pragma unroll
       for (int m = 0; m < kWaveBlock; ++m)
-        lds_dma16_buf(ckv_rsrc, dst + m * kCkvPitch, __builtin_amdgcn_readlane(co, m) + lane * 16);
+        lds_dma16_buf(ckv_rsrc, dst + m * kWavePitch, __builtin_amdgcn_readlane(co, m) + lane * 16);
       lds_dma16_buf(kpe_rsrc, dst + kWaveKpeOff, ko);
       lds_dma16_buf(kpe_rsrc, dst + kWaveKpeOff + 1024, ko + 64);
     } else {
@@ -1278,7 +1291,7 @@ __global__ __launch_bounds__(kWaveWaves * 64, 1) void dsa_attn_wave_kernel(AttnP
       ka += g * 16;
 #pragma unroll
       for (int m = 0; m < kWaveBlock; ++m)
-        lds_dma16((const char *)readlane64(ca, m) + lane * 16, dst + m * kCkvPitch);
+        lds_dma16((const char *)readlane64(ca, m) + lane * 16, dst + m * kWavePitch);
       lds_dma16((const char *)ka, dst + kWaveKpeOff);
       lds_dma16((const char *)ka + 64, dst + kWaveKpeOff + 1024);
     }
@@ -1296,7 +1309,7 @@ __global__ __launch_bounds__(kWaveWaves * 64, 1) void dsa_attn_wave_kernel(AttnP
     wait_vmcnt<0>();
   __builtin_amdgcn_s_barrier();
   bf16x8 q[18];
-  q_read18((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)(qstage + r16 * kCkvPitch + g * 16),
+  q_read18((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)(qstage + r16 * kWavePitch + g * 16),
            (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)(qstage + kQPePos + r16 * 128 + g * 16),
            q);
   __builtin_amdgcn_s_barrier();
@@ -1316,7 +1329,7 @@ __global__ __launch_bounds__(kWaveWaves * 64, 1) void dsa_attn_wave_kernel(AttnP
   // transposing V^T reads: lanes 4j..4j+3 of group g point at key
   // key_of_row(4g + j), 8-byte piece (lane & 3) of the feature block
   const int vrow = key_of_row(4 * g + (r16 >> 2));
-  const int voff = vrow * kCkvPitch + (r16 & 3) * 8;
+  const int voff = vrow * kWavePitch + (r16 & 3) * 8;
 
   for (int j = 0; j < my_blocks; ++j) {
     const int st = j & 1;
@@ -1336,7 +1349,7 @@ __global__ __launch_bounds__(kWaveWaves * 64, 1) void dsa_attn_wave_kernel(AttnP
     // one LDS round trip, not one each)
     f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
     {
-      const char *rowp = stg + qrow * kCkvPitch + g * 16;
+      const char *rowp = stg + qrow * kWavePitch + g * 16;
       const char *kp = stg + kWaveKpeOff + qrow * 16 + g * 256;
       bf16x8 ka[18];
 #pragma unroll
