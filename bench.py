@@ -226,8 +226,8 @@ def cpu_indexer_baseline(d, budget_s: float = 10.0):
             break
     return {"value": round(el / (n * rows) * T * 1e6, 1), "unit": "µs/call", "cores": threads,
             "kind": "port",
-            "sample": f"{n * rows} of {T} token rows (exact score over all positions + top-k, "
-                      f"{threads} threads, {el:.1f} s), scaled to the {T}-row call"}
+            "sample": f"{n * rows} token rows, cycling over the call's {T} (exact score over all "
+                      f"positions + top-k, {threads} threads, {el:.1f} s), scaled to the {T}-row call"}
 
 
 def graph_of(fn, n):
