@@ -820,6 +820,10 @@ __device__ __forceinline__ void pick_digit(const uint32_t *tot, uint32_t prefix,
   }
 }
 
+// v_writelane_b32 (the LLVM intrinsic; the compiler inserts the wait states
+// it needs after the VALU write of its SGPR source).
+extern "C" __device__ int amdgcn_writelane(int value, int lane, int old) __asm("llvm.amdgcn.writelane.i32");
+
 // Survivors of the first two radix passes that the register top-k ranks
 // directly; more take two more passes.
 constexpr int kMaxSurvivors = 256;
@@ -831,7 +835,7 @@ constexpr int kMaxSurvivors = 256;
 template <int KEYS>
 struct TopkShared {
   union {
-    uint32_t hist[kHistCopies * kHistPitch];
+    uint32_t hist[2][kHistCopies * kHistPitch];  // one per radix pass of the register top-k
     int32_t pos[KEYS];
   };
   uint64_t bits[KEYS / 64 > 0 ? KEYS / 64 : 1];    // selected
@@ -871,9 +875,9 @@ template <typename Shared, typename ForKeys>
 __device__ __forceinline__ void radix_pass(Shared &sh, int shift, ForKeys for_keys,
                                            uint32_t &prefix, uint32_t &mask, int &need,
                                            int phantom = 0) {
-  for (int i = threadIdx.x; i < kHistCopies * kHistPitch; i += kTopkThreads) sh.hist[i] = 0;
+  for (int i = threadIdx.x; i < kHistCopies * kHistPitch; i += kTopkThreads) sh.hist[0][i] = 0;
   __syncthreads();
-  uint32_t *myhist = sh.hist + (threadIdx.x & (kHistCopies - 1)) * kHistPitch;
+  uint32_t *myhist = sh.hist[0] + (threadIdx.x & (kHistCopies - 1)) * kHistPitch;
   const uint32_t pf = prefix, mk = mask;
   for_keys([&](uint32_t key, bool cand) {
     const uint32_t bin = (cand && (key & mk) == pf) ? ((key >> shift) & 255u) : 256u;
@@ -883,7 +887,7 @@ __device__ __forceinline__ void radix_pass(Shared &sh, int shift, ForKeys for_ke
   if (threadIdx.x < 256) {
     uint32_t c = 0;
 #pragma unroll 8
-    for (int j = 0; j < kHistCopies; ++j) c += sh.hist[j * kHistPitch + threadIdx.x];
+    for (int j = 0; j < kHistCopies; ++j) c += sh.hist[0][j * kHistPitch + threadIdx.x];
     if (threadIdx.x == 0 && prefix == 0) c -= (uint32_t)phantom;
     sh.tot[threadIdx.x] = c;
   }
@@ -899,28 +903,47 @@ __device__ __forceinline__ void radix_pass(Shared &sh, int shift, ForKeys for_ke
 // buffer load reads them as 0.0.
 constexpr uint32_t kPhantomKey = 0x80000000u;
 
-// One radix pass over the register-resident keys of a row.  Under prefix pf
-// (the digits above `shift` fixed so far) a key's digit is (k - pf) >> shift
-// when it matches the prefix (then below 256) and at least 256 otherwise, so
-// min(., 256) files every other key in the spare bin with three instructions
-// per key.  The `phantom` copies of kPhantomKey are taken out of their bin.
+// One radix pass over the register-resident keys of a row, into histogram
+// `hist`: with `zeroed` the caller zeroed it and passed a barrier since,
+// otherwise the pass zeroes it first.  Under prefix pf (the digits above
+// `shift` fixed so far) a key's digit is (k - pf) >> shift when it matches the
+// prefix (then below 256) and at least 256 otherwise.  The first pass (no
+// prefix) counts every key, min(., 256) keeping the branch out; later passes
+// issue atomics only for the keys under the prefix.  The copies are added by
+// all threads, four per bin (eight copies each, then a quad sum).  The
+// `phantom` copies of kPhantomKey are taken out of their bin.
 template <int EPT, typename Shared>
-__device__ __forceinline__ void radix_pass_regs(Shared &sh, int shift, const uint32_t (&key)[EPT],
-                                                uint32_t &prefix, uint32_t &mask, int &need,
-                                                int phantom) {
-  for (int i = threadIdx.x; i < kHistCopies * kHistPitch; i += kTopkThreads) sh.hist[i] = 0;
-  __syncthreads();
-  uint32_t *myhist = sh.hist + (threadIdx.x & (kHistCopies - 1)) * kHistPitch;
+__device__ __forceinline__ void radix_pass_regs(Shared &sh, uint32_t *hist, bool zeroed, int shift,
+                                                const uint32_t (&key)[EPT], uint32_t &prefix,
+                                                uint32_t &mask, int &need, int phantom) {
+  static_assert(kTopkThreads == 4 * 256, "four threads per bin in the copy sum");
+  if (!zeroed) {
+    for (int i = threadIdx.x; i < kHistCopies * kHistPitch; i += kTopkThreads) hist[i] = 0;
+    __syncthreads();
+  }
+  uint32_t *myhist = hist + (threadIdx.x & (kHistCopies - 1)) * kHistPitch;
   const uint32_t pf = prefix;
+  if (mask == 0) {  // first pass: every key counts
 #pragma unroll
-  for (int e = 0; e < EPT; ++e) atomicAdd(&myhist[min((key[e] - pf) >> shift, 256u)], 1u);
+    for (int e = 0; e < EPT; ++e) atomicAdd(&myhist[min((key[e] - pf) >> shift, 256u)], 1u);
+  } else {  // later passes: only the keys under the prefix (few) issue an atomic
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const uint32_t d = (key[e] - pf) >> shift;
+      if (d < 256u) atomicAdd(&myhist[d], 1u);
+    }
+  }
   __syncthreads();
-  if (threadIdx.x < 256) {
+  {
+    const int bin = threadIdx.x >> 2, q = threadIdx.x & 3;
+    constexpr int kPer = kHistCopies / 4;
     uint32_t c = 0;
-#pragma unroll 8
-    for (int j = 0; j < kHistCopies; ++j) c += sh.hist[j * kHistPitch + threadIdx.x];
-    if (threadIdx.x == min((kPhantomKey - pf) >> shift, 256u)) c -= (uint32_t)phantom;
-    sh.tot[threadIdx.x] = c;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) c += hist[(q * kPer + j) * kHistPitch + bin];
+    c += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)c, 0xb1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
+    c += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)c, 0x4e, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+    if (bin == (int)min((kPhantomKey - pf) >> shift, 256u)) c -= (uint32_t)phantom;
+    if (q == 0) sh.tot[bin] = c;
   }
   __syncthreads();
   if (threadIdx.x < 64) pick_digit(sh.tot, prefix, mask, shift, need, &sh.prefix, &sh.mask, &sh.need);
@@ -956,15 +979,19 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_idx_topk_kernel(IndexerParam
   {
     const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(row), 0, n * 4, 0x00020000);
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      const float f = __builtin_bit_cast(
-          float, __builtin_amdgcn_raw_buffer_load_b32(rs, tid * 4, e * kTopkThreads * 4, 0));
-      const uint32_t u = __builtin_bit_cast(uint32_t, f + 0.0f);
-      key[e] = u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
-    }
+    for (int e = 0; e < EPT; ++e)
+      key[e] = __builtin_amdgcn_raw_buffer_load_b32(rs, tid * 4, e * kTopkThreads * 4, 0);
   }
   const int phantom = KEYS - n;
   if (tid == 0) sh.n_cand = 0;  // ordered before its use by the passes' barriers
+  // both passes' histograms are zeroed while the key loads are in flight
+  for (int i = tid; i < 2 * kHistCopies * kHistPitch; i += kTopkThreads) (&sh.hist[0][0])[i] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, __builtin_bit_cast(float, key[e]) + 0.0f);
+    key[e] = u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
+  }
 
   // Two passes: the k-th largest key lies in the 16-bit bin `prefix`; keys
   // above the bin are all taken and `need` more come from its survivors.
@@ -972,7 +999,7 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_idx_topk_kernel(IndexerParam
   int need = p.topk, unused;
 #pragma unroll 1
   for (int shift = 24; shift >= 16; shift -= 8)
-    radix_pass_regs(sh, shift, key, prefix, mask, need, phantom);
+    radix_pass_regs(sh, sh.hist[shift == 24 ? 0 : 1], true, shift, key, prefix, mask, need, phantom);
 
   // Selection as a position bitmap, built from ballots of the registers
   // (64-bit word e*16 + wave holds key e of the wave's lanes: lane 2e + h
@@ -983,29 +1010,22 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_idx_topk_kernel(IndexerParam
   {
     const uint32_t hi = prefix | 0xffffu;  // keys above the bin
     uint32_t bw = 0;
-    uint64_t any = 0;
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
       const uint64_t ab = __ballot(key[e] > hi);
-      any |= __ballot(key[e] - prefix < 0x10000u);
-      bw = lane == 2 * e ? (uint32_t)ab : bw;
-      bw = lane == 2 * e + 1 ? (uint32_t)(ab >> 32) : bw;
-    }
-    if (lane < 2 * EPT) bits32[((lane >> 1) * kWaves + wave) * 2 + (lane & 1)] = bw;
-    if (any != 0) {  // uniform
-#pragma unroll
-      for (int e = 0; e < EPT; ++e) {
-        const uint64_t sb = __ballot(key[e] - prefix < 0x10000u);
-        if (sb != 0) {
-          int o = 0;
-          if (lane == 0) o = atomicAdd(&sh.n_cand, __popcll(sb));
-          o = __builtin_amdgcn_readfirstlane(o) +
-              __builtin_amdgcn_mbcnt_hi((uint32_t)(sb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)sb, 0));
-          if (((sb >> lane) & 1) && o < kMaxSurvivors)
-            sh.cand[o] = make_uint2(key[e], (uint32_t)(e * kTopkThreads + tid));
-        }
+      const uint64_t sb = __ballot(key[e] >= prefix) & ~ab;  // keys in the bin
+      bw = (uint32_t)amdgcn_writelane((int)(uint32_t)ab, 2 * e, (int)bw);
+      bw = (uint32_t)amdgcn_writelane((int)(uint32_t)(ab >> 32), 2 * e + 1, (int)bw);
+      if (sb != 0) {  // uniform
+        int o = 0;
+        if (lane == 0) o = atomicAdd(&sh.n_cand, __popcll(sb));
+        o = __builtin_amdgcn_readfirstlane(o) +
+            __builtin_amdgcn_mbcnt_hi((uint32_t)(sb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)sb, 0));
+        if (((sb >> lane) & 1) && o < kMaxSurvivors)
+          sh.cand[o] = make_uint2(key[e], (uint32_t)(e * kTopkThreads + tid));
       }
     }
+    if (lane < 2 * EPT) bits32[((lane >> 1) * kWaves + wave) * 2 + (lane & 1)] = bw;
   }
   __syncthreads();
   const int n_surv = sh.n_cand;
@@ -1019,9 +1039,15 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_idx_topk_kernel(IndexerParam
       if (i < ((n_surv + 15) & ~15)) {  // whole waves
         const uint2 me = sh.cand[min(i, n_surv - 1)];
         int r = 0;
-        for (int j = q; j < n_surv; j += 4) {
-          const uint2 c = sh.cand[j];
-          r += (int)c.y < n && (c.x > me.x || (c.x == me.x && c.y < me.y));
+        // four reads in flight per step (entries past the list count nothing)
+        for (int j0 = q; j0 < n_surv; j0 += 16) {
+          uint2 c[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) c[u] = sh.cand[min(j0 + 4 * u, kMaxSurvivors - 1)];
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            r += j0 + 4 * u < n_surv && (int)c[u].y < n &&
+                 (c[u].x > me.x || (c[u].x == me.x && c[u].y < me.y));
         }
         r += __builtin_amdgcn_update_dpp(0, r, 0xb1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
         r += __builtin_amdgcn_update_dpp(0, r, 0x4e, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
@@ -1035,7 +1061,7 @@ __global__ __launch_bounds__(kTopkThreads) void dsa_idx_topk_kernel(IndexerParam
     // keys above it are taken, and `need` of its ties, lowest positions first.
 #pragma unroll 1
     for (int shift = 8; shift >= 0; shift -= 8)
-      radix_pass_regs(sh, shift, key, prefix, mask, need, phantom);
+      radix_pass_regs(sh, sh.hist[0], false, shift, key, prefix, mask, need, phantom);
     // (Ties past n sit after every real position and `need` counts real
     // ones only, so they are never taken; the masking below clears the rest.)
 #pragma unroll
